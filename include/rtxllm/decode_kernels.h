@@ -1,0 +1,219 @@
+/* C-ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Drop-in for the reference's runtime/kernels/decode/decode_kernels.h: the
+ * rtxllm_launch_* entry points below keep the reference's names, argument order
+ * and meaning, with hipError_t / hipStream_t in place of the CUDA types. Every
+ * pointer argument is a device pointer into caller-owned memory; no entry point
+ * allocates, frees, copies or synchronises, so all are hipGraph-capturable.
+ * Each returns hipGetLastError() after its launches, or hipErrorInvalidValue
+ * for rejected arguments before launching anything.
+ *
+ * The rtxllm_* entry points without "launch" in their names have no
+ * counterpart in the reference; they carry the math of a real Llama decode step
+ * (pure y = W x, weighted RMSNorm, RoPE with a theta schedule, SiLU-gate
+ * multiply, Q5_K embedding gather, GQA attention over a paged fp16 KV cache,
+ * greedy argmax, batch-8 skinny GEMM) and the host-side pack helpers.
+ *
+ * Pack layouts (all row-major, rows x (cols / 256) blocks, cols % 256 == 0):
+ *   Q4_K raw 144 B, Q5_K 176 B, IQ2_S 82 B, IQ3_S 110 B GGUF blocks;
+ *   Q4_K split: 128 B payload stream + metadata stream of 64 B (predecoded,
+ *   8 x f32 (d*sc, dmin*m)), 32 B (half, the same as fp16), 20 B (compact:
+ *   f16 d, f16 dmin, u8 sc[8], u8 m[8]) or 16 B (native: the GGUF head).
+ */
+#ifndef RTXLLM_DECODE_KERNELS_H
+#define RTXLLM_DECODE_KERNELS_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== Reference-named entry points =====================================
+ * Feedback family: decode_kernels.h:38-101. act[c] is computed from
+ * logits[c % rows] normalised by inv_rms = rsqrt(mean(logits^2) + epsilon). */
+
+/* decode_kernels.h:38-44: activation[c] = logits[c % rows] * inv_rms. */
+hipError_t rtxllm_launch_rmsnorm_feedback(const float* logits, float* activation, uint32_t rows, uint32_t cols,
+                                          float epsilon, hipStream_t stream);
+
+/* decode_kernels.h:46-52: activation[c] = silu(logits[c % rows] * inv_rms). */
+hipError_t rtxllm_launch_silu_rmsnorm_feedback(const float* logits, float* activation, uint32_t rows,
+                                               uint32_t cols, float epsilon, hipStream_t stream);
+
+/* decode_kernels.h:54-61: activation[c] = n, silu_cache[c] = silu(n). */
+hipError_t rtxllm_launch_rmsnorm_feedback_with_silu_cache(const float* logits, float* activation,
+                                                          float* silu_cache, uint32_t rows, uint32_t cols,
+                                                          float epsilon, hipStream_t stream);
+
+/* decode_kernels.h:63-71: activation[c] = silu_cache[c % cache_cols] * n. */
+hipError_t rtxllm_launch_gated_silu_rmsnorm_feedback(const float* logits, const float* silu_cache,
+                                                     float* activation, uint32_t rows, uint32_t cache_cols,
+                                                     uint32_t cols, float epsilon, hipStream_t stream);
+
+/* decode_kernels.h:73-80: silu_cache[c] (+)= silu(n). cache_cols == 0 -> InvalidValue. */
+hipError_t rtxllm_launch_rmsnorm_silu_cache(const float* logits, float* silu_cache, uint32_t rows,
+                                            uint32_t cache_cols, float epsilon, uint32_t accumulate,
+                                            hipStream_t stream);
+
+/* decode_kernels.h:82-89: cache[c] (+)= n. cache_cols == 0 -> InvalidValue. */
+hipError_t rtxllm_launch_rmsnorm_cache(const float* logits, float* cache, uint32_t rows, uint32_t cache_cols,
+                                       float epsilon, uint32_t accumulate, hipStream_t stream);
+
+/* decode_kernels.h:91-101: up_cache[c] (+)= n; activation[c] = gate_cache[c] * up_cache[c]. */
+hipError_t rtxllm_launch_rmsnorm_cache_and_gated_product(const float* logits, const float* gate_cache,
+                                                         float* up_cache, float* activation, uint32_t rows,
+                                                         uint32_t cache_cols, uint32_t output_cols,
+                                                         float epsilon, uint32_t accumulate,
+                                                         hipStream_t stream);
+
+/* decode_kernels.h:319-325: token[0] = (argmax(logits[0:rows]) + token_offset) % vocab_size;
+ * ties -> lowest index. Null pointers or zero rows / vocab -> InvalidValue. */
+hipError_t rtxllm_launch_output_token_sample(const float* logits, uint32_t* token, uint32_t rows,
+                                             uint32_t vocab_size, uint32_t token_offset, hipStream_t stream);
+
+/* Matvec + decode side effects. Each *_decode* call runs y = W x over the
+ * launched rows, the KV side-write kv[(r*page_words + (token+r) % page_words) %
+ * kv_words] = y[r] for r < active_pages, then token = (argmax(y) + token + 1) %
+ * 32000. IQ/Q5_K calls clip to min(rows, rows_limit) rows. */
+
+/* decode_kernels.h:345-357. */
+hipError_t rtxllm_launch_q5k_matvec_decode_probe(const uint8_t* q5k_blocks, const float* activation,
+                                                 float* logits, float* kv, uint32_t* token, uint32_t rows,
+                                                 uint32_t cols, uint32_t rows_limit, uint32_t kv_words,
+                                                 uint32_t page_words, uint32_t active_pages,
+                                                 hipStream_t stream);
+
+/* decode_kernels.h:359-366: matvec only (no KV, no token). */
+hipError_t rtxllm_launch_iq2s_matvec_probe(const uint8_t* iq2s_blocks, const float* activation, float* logits,
+                                           uint32_t rows, uint32_t cols, uint32_t rows_limit,
+                                           hipStream_t stream);
+
+/* decode_kernels.h:368-380. */
+hipError_t rtxllm_launch_iq2s_matvec_decode_probe(const uint8_t* iq2s_blocks, const float* activation,
+                                                  float* logits, float* kv, uint32_t* token, uint32_t rows,
+                                                  uint32_t cols, uint32_t rows_limit, uint32_t kv_words,
+                                                  uint32_t page_words, uint32_t active_pages,
+                                                  hipStream_t stream);
+
+/* decode_kernels.h:382-394. */
+hipError_t rtxllm_launch_iq3s_matvec_decode_probe(const uint8_t* iq3s_blocks, const float* activation,
+                                                  float* logits, float* kv, uint32_t* token, uint32_t rows,
+                                                  uint32_t cols, uint32_t rows_limit, uint32_t kv_words,
+                                                  uint32_t page_words, uint32_t active_pages,
+                                                  hipStream_t stream);
+
+/* decode_kernels.h:424-513: Q4_K on raw 144 B blocks. The reference's variants
+ * (direct, shared, warp, warp_broadcast, _vec4, _vec4x2, _vec4x4) are CUDA
+ * implementation choices of one operation; all map to the one gfx950 kernel. */
+hipError_t rtxllm_launch_q4k_matvec_decode(const uint8_t* q4k_blocks, const float* activation, float* logits,
+                                           float* kv, uint32_t* token, uint32_t rows, uint32_t cols,
+                                           uint32_t kv_words, uint32_t page_words, uint32_t active_pages,
+                                           hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_shared(const uint8_t* q4k_blocks, const float* activation,
+                                                  float* logits, float* kv, uint32_t* token, uint32_t rows,
+                                                  uint32_t cols, uint32_t kv_words, uint32_t page_words,
+                                                  uint32_t active_pages, hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_warp(const uint8_t* q4k_blocks, const float* activation,
+                                                float* logits, float* kv, uint32_t* token, uint32_t rows,
+                                                uint32_t cols, uint32_t kv_words, uint32_t page_words,
+                                                uint32_t active_pages, hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_warp_broadcast(const uint8_t* q4k_blocks, const float* activation,
+                                                          float* logits, float* kv, uint32_t* token,
+                                                          uint32_t rows, uint32_t cols, uint32_t kv_words,
+                                                          uint32_t page_words, uint32_t active_pages,
+                                                          hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4(const uint8_t* q4k_blocks,
+                                                               const float* activation, float* logits,
+                                                               float* kv, uint32_t* token, uint32_t rows,
+                                                               uint32_t cols, uint32_t kv_words,
+                                                               uint32_t page_words, uint32_t active_pages,
+                                                               hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4x2(const uint8_t* q4k_blocks,
+                                                                 const float* activation, float* logits,
+                                                                 float* kv, uint32_t* token, uint32_t rows,
+                                                                 uint32_t cols, uint32_t kv_words,
+                                                                 uint32_t page_words, uint32_t active_pages,
+                                                                 hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4x4(const uint8_t* q4k_blocks,
+                                                                 const float* activation, float* logits,
+                                                                 float* kv, uint32_t* token, uint32_t rows,
+                                                                 uint32_t cols, uint32_t kv_words,
+                                                                 uint32_t page_words, uint32_t active_pages,
+                                                                 hipStream_t stream);
+
+/* decode_kernels.h:515-527: raw 144 B blocks for the quants, predecoded f32
+ * (d*sc, dmin*m) pairs (8 per block) for the scales. */
+hipError_t rtxllm_launch_q4k_matvec_decode_predecoded_vec4x4(const uint8_t* q4k_blocks,
+                                                             const float* q4k_scale_min_pairs,
+                                                             const float* activation, float* logits, float* kv,
+                                                             uint32_t* token, uint32_t rows, uint32_t cols,
+                                                             uint32_t kv_words, uint32_t page_words,
+                                                             uint32_t active_pages, hipStream_t stream);
+
+/* decode_kernels.h:529-583: Q4_K split resident layouts. */
+hipError_t rtxllm_launch_q4k_matvec_decode_split_predecoded_vec4x4(const uint8_t* q4k_payload,
+                                                                   const float* q4k_scale_min_pairs,
+                                                                   const float* activation, float* logits,
+                                                                   float* kv, uint32_t* token, uint32_t rows,
+                                                                   uint32_t cols, uint32_t kv_words,
+                                                                   uint32_t page_words, uint32_t active_pages,
+                                                                   hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_split_half_vec4x4(const uint8_t* q4k_payload,
+                                                             const uint16_t* q4k_scale_min_half_pairs,
+                                                             const float* activation, float* logits, float* kv,
+                                                             uint32_t* token, uint32_t rows, uint32_t cols,
+                                                             uint32_t kv_words, uint32_t page_words,
+                                                             uint32_t active_pages, hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_split_compact_vec4x4(const uint8_t* q4k_payload,
+                                                                const uint8_t* q4k_compact_meta,
+                                                                const float* activation, float* logits,
+                                                                float* kv, uint32_t* token, uint32_t rows,
+                                                                uint32_t cols, uint32_t kv_words,
+                                                                uint32_t page_words, uint32_t active_pages,
+                                                                hipStream_t stream);
+hipError_t rtxllm_launch_q4k_matvec_decode_split_native_vec4x4(const uint8_t* q4k_payload,
+                                                               const uint8_t* q4k_native_meta,
+                                                               const float* activation, float* logits,
+                                                               float* kv, uint32_t* token, uint32_t rows,
+                                                               uint32_t cols, uint32_t kv_words,
+                                                               uint32_t page_words, uint32_t active_pages,
+                                                               hipStream_t stream);
+
+/* ===== New entry points (no reference counterpart) ======================= */
+
+/* Format ids (payload / metadata layouts): 0 Q4_K raw, 1 split-predecoded,
+ * 2 split-half, 3 split-compact, 4 split-native, 5 Q5_K, 6 IQ2_S, 7 IQ3_S,
+ * 8 Q4_K raw + predecoded pairs. meta is null except for 1-4 and 8. */
+
+/* Dequantise to fp32 [rows][cols], bit-exact with the reference's per-element
+ * formulas (main.cpp:1133-1259). */
+hipError_t rtxllm_dequant_f32(int format, const uint8_t* payload, const uint8_t* meta, uint32_t rows,
+                              uint32_t cols, float* out, hipStream_t stream);
+
+/* y[rows] = W x (batch 1), no side effects. */
+hipError_t rtxllm_matvec(int format, const uint8_t* payload, const uint8_t* meta, const float* x, float* y,
+                         uint32_t rows, uint32_t cols, hipStream_t stream);
+
+/* Host-side helpers (no device work). */
+uint32_t rtxllm_format_payload_block_bytes(int format);
+uint32_t rtxllm_format_meta_block_bytes(int format);
+/* Split raw Q4_K blocks into a payload stream and format-`format` metadata
+ * (tools/bench/q4k_resident_pack.py:100-145). Host memory. Returns 0 or -1. */
+int rtxllm_q4k_split_pack(int format, const uint8_t* raw_blocks, size_t n_blocks, uint8_t* payload,
+                          uint8_t* meta);
+/* Seeded synthetic raw blocks (format 0, 5, 6, 7) into host memory, d/dmin =
+ * fp16(U[d_lo, d_hi]); threads <= 0 picks the hardware concurrency. */
+int rtxllm_synth_raw_blocks(int format, uint64_t seed, size_t n_blocks, float d_lo, float d_hi,
+                            uint8_t* out, int threads);
+/* Seeded N(mean, std^2) fp32 values, or fp16 bits of them. */
+int rtxllm_synth_normal_f32(uint64_t seed, size_t n, float mean, float stddev, float* out, int threads);
+int rtxllm_synth_normal_f16(uint64_t seed, size_t n, float mean, float stddev, uint16_t* out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,107 @@
+"""ctypes binding of build/librtxllm.so, the gfx950 decode library's C-ABI.
+
+The library is the product: nothing here falls back to another implementation.
+If the shared object is missing or fails to load, ``lib()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_ROOT / "build" / "librtxllm.so"
+
+_P = c_void_p  # device or host pointer
+_U = c_uint32
+_S = c_void_p  # hipStream_t
+
+# name -> argtypes. Every launcher returns hipError_t (int).
+_LAUNCH_SIGS: dict[str, list] = {
+    "rtxllm_launch_rmsnorm_feedback": [_P, _P, _U, _U, c_float, _S],
+    "rtxllm_launch_silu_rmsnorm_feedback": [_P, _P, _U, _U, c_float, _S],
+    "rtxllm_launch_rmsnorm_feedback_with_silu_cache": [_P, _P, _P, _U, _U, c_float, _S],
+    "rtxllm_launch_gated_silu_rmsnorm_feedback": [_P, _P, _P, _U, _U, _U, c_float, _S],
+    "rtxllm_launch_rmsnorm_silu_cache": [_P, _P, _U, _U, c_float, _U, _S],
+    "rtxllm_launch_rmsnorm_cache": [_P, _P, _U, _U, c_float, _U, _S],
+    "rtxllm_launch_rmsnorm_cache_and_gated_product": [_P, _P, _P, _P, _U, _U, _U, c_float, _U, _S],
+    "rtxllm_launch_output_token_sample": [_P, _P, _U, _U, _U, _S],
+    "rtxllm_launch_q5k_matvec_decode_probe": [_P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _S],
+    "rtxllm_launch_iq2s_matvec_probe": [_P, _P, _P, _U, _U, _U, _S],
+    "rtxllm_launch_iq2s_matvec_decode_probe": [_P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _S],
+    "rtxllm_launch_iq3s_matvec_decode_probe": [_P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _S],
+    "rtxllm_dequant_f32": [c_int, _P, _P, _U, _U, _P, _S],
+    "rtxllm_matvec": [c_int, _P, _P, _P, _P, _U, _U, _S],
+}
+for _name in (
+    "rtxllm_launch_q4k_matvec_decode",
+    "rtxllm_launch_q4k_matvec_decode_shared",
+    "rtxllm_launch_q4k_matvec_decode_warp",
+    "rtxllm_launch_q4k_matvec_decode_warp_broadcast",
+    "rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4",
+    "rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4x2",
+    "rtxllm_launch_q4k_matvec_decode_warp_broadcast_vec4x4",
+):
+    _LAUNCH_SIGS[_name] = [_P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _S]
+for _name in (
+    "rtxllm_launch_q4k_matvec_decode_predecoded_vec4x4",
+    "rtxllm_launch_q4k_matvec_decode_split_predecoded_vec4x4",
+    "rtxllm_launch_q4k_matvec_decode_split_half_vec4x4",
+    "rtxllm_launch_q4k_matvec_decode_split_compact_vec4x4",
+    "rtxllm_launch_q4k_matvec_decode_split_native_vec4x4",
+):
+    _LAUNCH_SIGS[_name] = [_P, _P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _S]
+
+# name -> (restype, argtypes) for host helpers.
+_HOST_SIGS: dict[str, tuple] = {
+    "rtxllm_format_payload_block_bytes": (c_uint32, [c_int]),
+    "rtxllm_format_meta_block_bytes": (c_uint32, [c_int]),
+    "rtxllm_q4k_split_pack": (c_int, [c_int, _P, c_size_t, _P, _P]),
+    "rtxllm_synth_raw_blocks": (c_int, [c_int, c_uint64, c_size_t, c_float, c_float, _P, c_int]),
+    "rtxllm_synth_normal_f32": (c_int, [c_uint64, c_size_t, c_float, c_float, _P, c_int]),
+    "rtxllm_synth_normal_f16": (c_int, [c_uint64, c_size_t, c_float, c_float, _P, c_int]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load build/librtxllm.so (once) and declare every exported signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.is_file():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C {PKG_ROOT}` "
+                "(or __graft_entry__.build()); there is no fallback path"
+            )
+        handle = ctypes.CDLL(os.fspath(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+        for name, argtypes in _LAUNCH_SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = c_int
+            fn.argtypes = argtypes
+        for name, (restype, argtypes) in _HOST_SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def exported_names() -> list[str]:
+    return sorted(list(_LAUNCH_SIGS) + list(_HOST_SIGS))
+
+
+class HipError(RuntimeError):
+    def __init__(self, name: str, code: int):
+        super().__init__(f"{name} returned hipError_t {code}")
+        self.code = code
+
+
+def check(name: str, code: int) -> None:
+    if code != 0:
+        raise HipError(name, code)
+
+
+__all__ = ["lib", "check", "HipError", "exported_names", "LIB_PATH", "c_uint16"]
