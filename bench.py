@@ -127,15 +127,19 @@ def main() -> int:
             c.meta = base.meta.clone() if base.meta is not None else None
             copies.append(c)
         x = ops.to_dev(packs.normal_f32(seed + 0x100, cols), dev)
+        xq = ops.stage(x)
         y = torch.empty(rows, dtype=torch.float32, device=dev)
-        runs.append((name, fmt, rows, cols, copies, x, y))
+        runs.append((name, fmt, rows, cols, copies, (x, xq), y))
 
     # One step = every matvec once; successive steps rotate the weight copies.
     n_rot = max(len(r[4]) for r in runs)
 
     def launch_step(k: int) -> None:
-        for _, _, _, _, copies, x, y in runs:
-            ops.matvec(copies[k % len(copies)], x, y)
+        # every activation is staged once per step, then each matvec reads it
+        for _, _, _, _, _, (x, xq), _ in runs:
+            ops.stage(x, out=xq)
+        for _, _, _, _, copies, (x, xq), y in runs:
+            ops.matvec_xq(copies[k % len(copies)], xq, y)
 
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
@@ -151,11 +155,11 @@ def main() -> int:
 
     # Per-matvec kernel time: one graph per matvec over its copies.
     per = {}
-    for name, fmt, rows, cols, copies, x, y in runs:
+    for name, fmt, rows, cols, copies, (x, xq), y in runs:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
             for c in copies:
-                ops.matvec(c, x, y)
+                ops.matvec_xq(c, xq, y)
         torch.cuda.synchronize()
         for _ in range(2):
             g.replay()
@@ -204,7 +208,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32-accumulate over q4k/q5k/iq2s/iq3s",
+        "dtype": "int8 dot4 (weight codes x 2-digit int8 activation) + f32 scales",
         "data": "synthetic seeded packs (splitmix64), x ~ N(0,1)",
         "config": {"workload": "matvec set: " + ", ".join(r[0] for r in runs), "batch": 1,
                    "wall_s": round(wall, 3)},

@@ -193,9 +193,26 @@ hipError_t rtxllm_launch_q4k_matvec_decode_split_native_vec4x4(const uint8_t* q4
 hipError_t rtxllm_dequant_f32(int format, const uint8_t* payload, const uint8_t* meta, uint32_t rows,
                               uint32_t cols, float* out, hipStream_t stream);
 
-/* y[rows] = W x (batch 1), no side effects. */
+/* y[rows] = W x (batch 1), no side effects. x is fp32; each wave stages the
+ * columns it owns itself (see rtxllm_stage_activation for the staging rule). */
 hipError_t rtxllm_matvec(int format, const uint8_t* payload, const uint8_t* meta, const float* x, float* y,
                          uint32_t rows, uint32_t cols, hipStream_t stream);
+
+/* Staged activation ("xq"): x is cut into 16-value groups; each group is kept as
+ * 15-bit fixed point X_j = rint(x_j * 16256 / max|x|) split into int8 digits
+ * X_j = 128 H_j + L_j, plus the group scale s = max|x| / 16256 and the group
+ * sum s * sum(X). Layout of one buffer of rtxllm_xq_bytes(cols) bytes: H[cols],
+ * L[cols] (int8), s[cols/16], sum[cols/16] (f32). The matvec kernels multiply
+ * the weight codes with the digits through exact integer dot products, so the
+ * staging rounding (relative step 6.2e-5 of the group maximum) is the only
+ * deviation from an fp32 product. */
+size_t rtxllm_xq_bytes(uint32_t cols);
+/* xq = stage(x * weight) (weight may be null: stage x). cols % 256 == 0. */
+hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t cols, void* xq,
+                                   hipStream_t stream);
+/* y[rows] = W x_hat for a staged x (the layer pipeline's matvec). */
+hipError_t rtxllm_matvec_xq(int format, const uint8_t* payload, const uint8_t* meta, const void* xq, float* y,
+                            uint32_t rows, uint32_t cols, hipStream_t stream);
 
 /* Host-side helpers (no device work). */
 uint32_t rtxllm_format_payload_block_bytes(int format);

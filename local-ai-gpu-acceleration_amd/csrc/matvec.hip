@@ -2,49 +2,81 @@
 #include "rtxllm/decode_kernels.h"
 
 #include "internal.h"
-#include "matvec.cuh"
+#include "mv.cuh"
 
 namespace rtxllm {
 namespace {
 
-constexpr int kRowsPerGroup = 4;
+constexpr int kTile = 4;
 
-// Waves per workgroup: enough lanes to cover a row's 32-weight units once,
-// capped at 8 waves (units = 8 per 256-column block).
-inline unsigned waves_for(std::uint32_t cols) {
-  const std::uint32_t units = (cols / 256u) * 8u;
-  std::uint32_t w = (units + 63u) / 64u;
-  if (w < 1u) w = 1u;
-  if (w > 8u) w = 8u;
-  return w;
+[[maybe_unused]] int num_cus() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cached = n;
+    else
+      cached = 256;
+  }
+  return cached;
 }
 
-template <int FMT>
-hipError_t launch_matvec_fmt(const QTensor& w, const float* x, float* y, std::uint32_t row_count,
-                             const KvSideWrite& side, hipStream_t stream) {
-  const dim3 grid((row_count + kRowsPerGroup - 1) / kRowsPerGroup);
-  const dim3 block(64u * waves_for(w.cols));
-  hipLaunchKernelGGL((matvec_b1_kernel<FMT, kRowsPerGroup>), grid, block, 0, stream, w, x, y, row_count, side);
+// Launch geometry of mv_kernel, from a sweep on MI355X at the 8B shapes: one
+// unit (32 columns) per lane for rows of up to 16384 columns (two beyond),
+// ks = ceil(units / 64) waves per row, nrg = 4 / ks row groups per workgroup
+// (at least 1), and one 4-row tile per row group: many small workgroups keep
+// enough loads in flight and the dispatcher's tail short.
+struct MvGeom {
+  int upl;
+  unsigned ks, nrg, grid;
+};
+
+bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, MvGeom& g) {
+  (void)fmt;
+  const std::uint32_t units = cols / 32u;
+  g.upl = units > 512u ? 2 : 1;
+  g.ks = (units + 64u * g.upl - 1u) / (64u * g.upl);
+  if (g.ks > static_cast<unsigned>(kMaxKs)) return false;
+  g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
+  const std::uint32_t tiles = (rows + tile - 1) / tile;
+  const std::uint32_t grid = (tiles + g.nrg - 1) / g.nrg;
+  g.grid = grid < 1u ? 1u : (grid > 1048576u ? 1048576u : grid);
+  return true;
+}
+
+template <int FMT, bool SELF, class Epi>
+hipError_t launch_mv_fmt(const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
+                         hipStream_t stream) {
+  MvGeom g;
+  if (!mv_geom(FMT, row_count, w.cols, kTile, g)) return hipErrorInvalidValue;
+  const dim3 grid(g.grid), block(64u * g.ks * g.nrg);
+  if (g.upl == 2) {
+    hipLaunchKernelGGL((mv_kernel<FMT, 2, kTile, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
+  } else {
+    hipLaunchKernelGGL((mv_kernel<FMT, 1, kTile, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_matvec(int fmt, const QTensor& w, const float* x, float* y, std::uint32_t row_count,
-                         const KvSideWrite& side, hipStream_t stream) {
+template <bool SELF, class Epi>
+hipError_t launch_mv(int fmt, const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
+                     hipStream_t stream) {
   switch (fmt) {
-    case RTXLLM_FMT_Q4K_RAW: return launch_matvec_fmt<RTXLLM_FMT_Q4K_RAW>(w, x, y, row_count, side, stream);
+    case RTXLLM_FMT_Q4K_RAW: return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_SPLIT_PREDECODED:
-      return launch_matvec_fmt<RTXLLM_FMT_Q4K_SPLIT_PREDECODED>(w, x, y, row_count, side, stream);
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_PREDECODED, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_SPLIT_HALF:
-      return launch_matvec_fmt<RTXLLM_FMT_Q4K_SPLIT_HALF>(w, x, y, row_count, side, stream);
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_HALF, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_SPLIT_COMPACT:
-      return launch_matvec_fmt<RTXLLM_FMT_Q4K_SPLIT_COMPACT>(w, x, y, row_count, side, stream);
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_COMPACT, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
-      return launch_matvec_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(w, x, y, row_count, side, stream);
-    case RTXLLM_FMT_Q5K: return launch_matvec_fmt<RTXLLM_FMT_Q5K>(w, x, y, row_count, side, stream);
-    case RTXLLM_FMT_IQ2S: return launch_matvec_fmt<RTXLLM_FMT_IQ2S>(w, x, y, row_count, side, stream);
-    case RTXLLM_FMT_IQ3S: return launch_matvec_fmt<RTXLLM_FMT_IQ3S>(w, x, y, row_count, side, stream);
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q5K: return launch_mv_fmt<RTXLLM_FMT_Q5K, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_IQ2S: return launch_mv_fmt<RTXLLM_FMT_IQ2S, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_IQ3S: return launch_mv_fmt<RTXLLM_FMT_IQ3S, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_RAW_PREDECODED:
-      return launch_matvec_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED>(w, x, y, row_count, side, stream);
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED, SELF>(w, xs, row_count, epi, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -165,8 +197,8 @@ hipError_t decode_call(int fmt, const std::uint8_t* payload, const std::uint8_t*
       token == nullptr || (needs_meta(fmt) && meta == nullptr) || !pointers_ok(fmt, payload, meta, x))
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
-  const KvSideWrite side{kv, token, kv_words, page_words, active_pages};
-  const hipError_t st = launch_matvec(fmt, w, x, y, launched_rows, side, stream);
+  const EpiDecode<kTile> epi{y, kv, token, kv_words, page_words, active_pages};
+  const hipError_t st = launch_mv<true>(fmt, w, XSrc{XQ{}, x}, launched_rows, epi, stream);
   if (st != hipSuccess) return st;
   return launch_argmax_token(y, token, launched_rows, 0, 32000u, 0u, stream);
 }
@@ -207,7 +239,19 @@ extern "C" hipError_t rtxllm_matvec(int format, const std::uint8_t* payload, con
       (needs_meta(format) && meta == nullptr) || !pointers_ok(format, payload, meta, x))
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
-  return launch_matvec(format, w, x, y, rows, KvSideWrite{}, stream);
+  return launch_mv<true>(format, w, XSrc{XQ{}, x}, rows, EpiStore<kTile>{y}, stream);
+}
+
+extern "C" std::size_t rtxllm_xq_bytes(std::uint32_t cols) { return xq_bytes(cols); }
+
+extern "C" hipError_t rtxllm_matvec_xq(int format, const std::uint8_t* payload, const std::uint8_t* meta,
+                                       const void* xq, float* y, std::uint32_t rows, std::uint32_t cols,
+                                       hipStream_t stream) {
+  if (!shape_ok(rows, cols) || payload == nullptr || xq == nullptr || y == nullptr ||
+      (needs_meta(format) && meta == nullptr) || !pointers_ok(format, payload, meta, xq))
+    return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  return launch_mv<false>(format, w, XSrc{xq_view(xq, cols), nullptr}, rows, EpiStore<kTile>{y}, stream);
 }
 
 // ---- reference-named matvec launchers --------------------------------------
@@ -308,6 +352,6 @@ extern "C" hipError_t rtxllm_launch_iq2s_matvec_probe(const std::uint8_t* iq2s_b
       logits == nullptr || !pointers_ok(RTXLLM_FMT_IQ2S, iq2s_blocks, nullptr, activation))
     return hipErrorInvalidValue;
   const QTensor w{iq2s_blocks, nullptr, rows, cols};
-  return launch_matvec(RTXLLM_FMT_IQ2S, w, activation, logits, clip_rows(rows, rows_limit), KvSideWrite{},
-                       stream);
+  return launch_mv<true>(RTXLLM_FMT_IQ2S, w, XSrc{XQ{}, activation}, clip_rows(rows, rows_limit),
+                         EpiStore<kTile>{logits}, stream);
 }

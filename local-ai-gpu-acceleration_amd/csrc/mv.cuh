@@ -1,0 +1,549 @@
+// Batch-1 dequant-matvec core for the GGUF resident-pack layouts (gfx950).
+//
+// Work split. A row of `cols` values is cut into 32-value units (Q4_K/Q5_K: 16
+// payload bytes = one half of a 64-value group; IQ2_S/IQ3_S: one 32-value
+// sub-block). Lane `lane` of a wave owns units lane, lane + 64, ... of its
+// column slice for the whole launch and keeps their staged activation digits
+// in registers (two 16-value groups per unit), so x is read once per wave and
+// never again. Waves then sweep tiles of TILE consecutive rows: for each row
+// every lane loads only its own units' bytes (16-byte nontemporal loads for
+// the K-quants, coalesced across the 64 lanes) and accumulates
+//   Q4_K/Q5_K:  S_sub * (s_x * sum(q * X)) - M_sub * sum(x_hat)
+//   IQ2_S/3_S:  scale_sub * s_x * sum(+-grid * X)
+// with the integer sums from v_dot4_i32_i8 on int8 weight codes and the int8
+// activation digits. Per-row partial sums of a tile are folded across the 64
+// lanes by a butterfly transpose-reduce, which leaves row r of the tile in
+// lanes [r * 64/TILE, (r+1) * 64/TILE); wide rows (cols > 4096) split their
+// columns over KS waves of one workgroup and add the KS partials through LDS.
+// The epilogue functor receives the finished tile and writes y (plus any fused
+// work). Summation order is fixed, so results are deterministic run to run.
+#pragma once
+
+#include "common.h"
+#include "iq_grids.h"
+#include "xq.h"
+
+namespace rtxllm {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+struct QTensor {
+  const std::uint8_t* payload;  // raw blocks, or the Q4_K split payload stream
+  const std::uint8_t* meta;     // Q4_K split metadata stream, else unused
+  std::uint32_t rows;
+  std::uint32_t cols;
+};
+
+// Activation source: staged digits, or fp32 x staged by each wave itself.
+struct XSrc {
+  XQ xq;
+  const float* x;
+};
+
+static __constant__ std::uint16_t kIq2sGridDev[1024] = {RTXLLM_IQ2S_GRID_VALUES};
+static __constant__ std::uint32_t kIq3sGridDev[512] = {RTXLLM_IQ3S_GRID_VALUES};
+
+__device__ __forceinline__ u32x4 ldnt16(const std::uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ std::uint32_t ldnt_u16(const std::uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const std::uint16_t*>(p));
+}
+__device__ __forceinline__ std::uint32_t ldnt_u8(const std::uint8_t* p) {
+  return __builtin_nontemporal_load(p);
+}
+// Four bytes at a 2-byte aligned address.
+__device__ __forceinline__ std::uint32_t ldnt_u32_a2(const std::uint8_t* p) {
+  return ldnt_u16(p) | (ldnt_u16(p + 2) << 16);
+}
+
+constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S; }
+constexpr bool fmt_is_raw_q4k(int f) { return f == RTXLLM_FMT_Q4K_RAW || f == RTXLLM_FMT_Q4K_RAW_PREDECODED; }
+
+// ---- LDS codebooks for the IQ formats ---------------------------------------
+// grid2: IQ2_S index -> eight magnitude bytes 2l+1; grid3: IQ3_S index -> four
+// magnitude bytes; sign: sign byte -> (M_lo, M_hi, E_lo, E_hi), M = 0xFF in the
+// byte of every set bit, E = M & 0x01. A signed int8 weight is (mag ^ M) + E:
+// magnitudes are >= 1, so the per-byte add never carries.
+struct IqLds {
+  uint2 grid2[1024];
+  std::uint32_t grid3[512];
+  uint4 sign[256];
+};
+
+// The workgroup's codebook copy (only IQ instantiations reference it).
+template <int FMT>
+__device__ __forceinline__ IqLds& iq_lds() {
+  __shared__ IqLds t;
+  return t;
+}
+
+template <int FMT>
+__device__ void iq_lds_build(IqLds& t) {
+  for (std::uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) {
+    std::uint32_t m0 = 0u, m1 = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m0 |= ((i >> j) & 1u) ? (0xFFu << (8 * j)) : 0u;
+      m1 |= ((i >> (j + 4)) & 1u) ? (0xFFu << (8 * j)) : 0u;
+    }
+    t.sign[i] = make_uint4(m0, m1, m0 & 0x01010101u, m1 & 0x01010101u);
+  }
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    for (std::uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) {
+      const std::uint32_t w = kIq2sGridDev[i];
+      std::uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo |= (2u * ((w >> (2 * j)) & 3u) + 1u) << (8 * j);
+        hi |= (2u * ((w >> (2 * j + 8)) & 3u) + 1u) << (8 * j);
+      }
+      t.grid2[i] = make_uint2(lo, hi);
+    }
+  } else {
+    for (std::uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) t.grid3[i] = kIq3sGridDev[i];
+  }
+}
+
+// ---- per-format unit load + compute ------------------------------------------
+
+// Hardware fp16 -> fp32 (exact for every finite and infinite input; a NaN stays
+// a NaN). The bit-exact dequant path keeps the reference's NaN rule instead.
+__device__ __forceinline__ float h2f(std::uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits & 0xFFFFu)));
+}
+
+// Byte offsets, relative to the start of a row, of the fields lane's unit
+// (block b, unit k) reads; fixed for the whole launch. Rows are addressed by a
+// wave-uniform base pointer, so every load is (uniform base + lane offset).
+struct UnitOff {
+  std::uint32_t o[5];
+  std::uint32_t g;      // K-quants: 64-value group k >> 1
+};
+
+template <int FMT>
+struct FmtBytes {
+  // Bytes per block in the payload stream and the metadata stream.
+  static constexpr std::uint32_t payload = FMT == RTXLLM_FMT_Q5K ? 176u
+                                           : FMT == RTXLLM_FMT_IQ2S ? 82u
+                                           : FMT == RTXLLM_FMT_IQ3S ? 110u
+                                           : fmt_is_raw_q4k(FMT) ? 144u : 128u;
+  static constexpr std::uint32_t meta = FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED ? 64u
+                                        : FMT == RTXLLM_FMT_Q4K_SPLIT_HALF ? 32u
+                                        : FMT == RTXLLM_FMT_Q4K_SPLIT_COMPACT ? 20u
+                                        : FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE ? 16u : 0u;
+};
+
+template <int FMT>
+__device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k) {
+  UnitOff u{};
+  const std::uint32_t pb = b * FmtBytes<FMT>::payload, mb = b * FmtBytes<FMT>::meta, g = k >> 1;
+  u.g = g;
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    u.o[0] = pb;                 // d
+    u.o[1] = pb + 2u + 4u * k;   // qs (grid low bytes)
+    u.o[2] = pb + 34u + 4u * k;  // sign bytes
+    u.o[3] = pb + 66u + k;       // qh
+    u.o[4] = pb + 74u + k;       // scale nibbles
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
+    u.o[0] = pb;                   // d
+    u.o[1] = pb + 2u + 8u * k;     // qs (8 grid low bytes)
+    u.o[2] = pb + 74u + 4u * k;    // sign bytes
+    u.o[3] = pb + 66u + k;         // qh
+    u.o[4] = pb + 106u + (k >> 1); // scale nibbles
+  } else if constexpr (FMT == RTXLLM_FMT_Q5K) {
+    u.o[0] = pb + 48u + 16u * k;          // qs
+    u.o[1] = pb;                          // head
+    u.o[2] = pb + 16u + 16u * (k & 1u);   // qh
+  } else {
+    u.o[0] = pb + (fmt_is_raw_q4k(FMT) ? 16u : 0u) + 16u * k;  // payload quants
+    if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) u.o[1] = pb;
+    else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE) u.o[1] = mb;
+    else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED)
+      u.o[1] = mb + 16u * g;
+    else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) u.o[1] = mb + 8u * g;
+    else {  // split-compact
+      u.o[1] = mb;
+      u.o[2] = mb + 4u + 2u * g;
+      u.o[3] = mb + 12u + 2u * g;
+    }
+  }
+  return u;
+}
+
+// Bytes of one (row, unit) kept in registers between the load and compute phases.
+struct UnitRaw {
+  std::uint32_t a[4];  // K-quants: payload quants; IQ2_S: qs, signs; IQ3_S: qs0, qs1, signs
+  std::uint32_t b[4];  // K-quants: native head / metadata
+  std::uint32_t c[4];  // Q5_K: qh bytes; IQ: d, qh, scale byte
+};
+
+// Value groups (16-value staging groups) covered by unit k of block b.
+template <int FMT>
+__device__ __forceinline__ void unit_groups(std::uint32_t b, std::uint32_t k, std::uint32_t& g0, std::uint32_t& g1) {
+  if constexpr (fmt_is_iq(FMT)) {
+    g0 = 16u * b + 2u * k;
+    g1 = g0 + 1u;
+  } else {
+    const std::uint32_t g = k >> 1, h = k & 1u;
+    g0 = 16u * b + 4u * g + h;  // low nibbles: values 64g + 16h + [0, 16)
+    g1 = g0 + 2u;               // high nibbles: values 64g + 32 + 16h + [0, 16)
+  }
+}
+
+// rp / rm: this row's start in the payload / metadata stream (wave-uniform).
+template <int FMT>
+__device__ __forceinline__ void unit_load(const std::uint8_t* rp, const std::uint8_t* rm, const UnitOff& u,
+                                          UnitRaw& r) {
+  if constexpr (FMT == RTXLLM_FMT_Q5K) {
+    const u32x4 q = ldnt16(rp + u.o[0]);
+    const u32x4 h = ldnt16(rp + u.o[1]);
+    const u32x4 qh = ldnt16(rp + u.o[2]);
+    r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
+    r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
+    r.c[0] = qh.x, r.c[1] = qh.y, r.c[2] = qh.z, r.c[3] = qh.w;
+  } else if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    r.c[0] = ldnt_u16(rp + u.o[0]);
+    r.a[0] = ldnt_u32_a2(rp + u.o[1]);
+    r.a[1] = ldnt_u32_a2(rp + u.o[2]);
+    r.c[1] = ldnt_u8(rp + u.o[3]);
+    r.c[2] = ldnt_u8(rp + u.o[4]);
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
+    r.c[0] = ldnt_u16(rp + u.o[0]);
+    r.a[0] = ldnt_u32_a2(rp + u.o[1]);
+    r.a[1] = ldnt_u32_a2(rp + u.o[1] + 4u);
+    r.a[2] = ldnt_u32_a2(rp + u.o[2]);
+    r.c[1] = ldnt_u8(rp + u.o[3]);
+    r.c[2] = ldnt_u8(rp + u.o[4]);
+  } else {
+    const u32x4 q = ldnt16(rp + u.o[0]);
+    r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
+    if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) {
+      const u32x4 h = ldnt16(rp + u.o[1]);
+      r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
+    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE || FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED ||
+                         FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
+      const u32x4 h = ldnt16(rm + u.o[1]);
+      r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
+    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
+      const u32x2 h = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rm + u.o[1]));
+      r.b[0] = h.x, r.b[1] = h.y;
+    } else {  // split-compact: f16 d, f16 dmin, u8 sc[8], u8 m[8]
+      r.b[0] = __builtin_nontemporal_load(reinterpret_cast<const std::uint32_t*>(rm + u.o[1]));
+      r.b[1] = ldnt_u16(rm + u.o[2]);
+      r.b[2] = ldnt_u16(rm + u.o[3]);
+    }
+  }
+}
+
+// (S, M) of sub-blocks 2g and 2g+1 from the native 16-byte head (d, dmin, 12
+// packed 6-bit scale/min bytes), branch-free: all eight scales and mins are
+// unpacked byte-parallel (get_scale_min_k4 for j < 4 and j >= 4), then the
+// lane's two bytes are picked by its fixed group g.
+__device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uint32_t g, float& s0, float& m0,
+                                              float& s1, float& m1) {
+  const std::uint32_t sc03 = h[1] & 0x3F3F3F3Fu;
+  const std::uint32_t m03 = h[2] & 0x3F3F3F3Fu;
+  const std::uint32_t sc47 = (h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u);
+  const std::uint32_t m47 = ((h[3] >> 4) & 0x0F0F0F0Fu) | ((h[2] >> 2) & 0x30303030u);
+  const std::uint32_t sh = 16u * (g & 1u);
+  const std::uint32_t sc = (g < 2u ? sc03 : sc47) >> sh;
+  const std::uint32_t mn = (g < 2u ? m03 : m47) >> sh;
+  const float d = h2f(h[0]), dmin = h2f(h[0] >> 16);
+  s0 = d * static_cast<float>(sc & 0xFFu);
+  s1 = d * static_cast<float>((sc >> 8) & 0xFFu);
+  m0 = dmin * static_cast<float>(mn & 0xFFu);
+  m1 = dmin * static_cast<float>((mn >> 8) & 0xFFu);
+}
+
+template <int FMT>
+__device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u, std::uint32_t k, const XG& x0,
+                                              const XG& x1, const IqLds* t) {
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    int ah[2] = {0, 0}, al[2] = {0, 0};
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
+      const uint2 gm = t->grid2[idx];
+      const uint4 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
+      const std::uint32_t w0 = (gm.x ^ sm.x) + sm.z;
+      const std::uint32_t w1 = (gm.y ^ sm.y) + sm.w;
+      const XG& xg = grp < 2 ? x0 : x1;
+      const int o = (grp & 1) * 2, s = grp >> 1;
+      ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w0), static_cast<int>(xg.h[o]), ah[s], false);
+      ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w1), static_cast<int>(xg.h[o + 1]), ah[s], false);
+      al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w0), static_cast<int>(xg.l[o]), al[s], false);
+      al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w1), static_cast<int>(xg.l[o + 1]), al[s], false);
+    }
+    const float d = h2f(r.c[0]);
+    const float s0 = d * (0.5f + static_cast<float>(r.c[2] & 15u)) * 0.25f;
+    const float s1 = d * (0.5f + static_cast<float>(r.c[2] >> 4)) * 0.25f;
+    return (s0 * x0.s) * static_cast<float>(ah[0] * 128 + al[0]) +
+           (s1 * x1.s) * static_cast<float>(ah[1] * 128 + al[1]);
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
+    int ah[2] = {0, 0}, al[2] = {0, 0};
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const uint4 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
+      const XG& xg = grp < 2 ? x0 : x1;
+      const int o = (grp & 1) * 2, s = grp >> 1;
+#pragma unroll
+      for (int pair = 0; pair < 2; ++pair) {
+        const int sel = 2 * grp + pair;
+        const std::uint32_t qb = (r.a[sel >> 2] >> (8 * (sel & 3))) & 0xFFu;
+        const std::uint32_t idx = qb | (((r.c[1] >> sel) & 1u) << 8);
+        const std::uint32_t w = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z);
+        ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(xg.h[o + pair]), ah[s], false);
+        al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(xg.l[o + pair]), al[s], false);
+      }
+    }
+    const std::uint32_t nib = (k & 1u) ? (r.c[2] >> 4) : (r.c[2] & 15u);
+    const float scale = h2f(r.c[0]) * static_cast<float>(1u + 2u * nib);
+    return (scale * x0.s) * static_cast<float>(ah[0] * 128 + al[0]) +
+           (scale * x1.s) * static_cast<float>(ah[1] * 128 + al[1]);
+  } else {
+    const std::uint32_t g = u.g;
+    std::uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = r.a[i] & 0x0F0F0F0Fu;
+      hi[i] = (r.a[i] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (FMT == RTXLLM_FMT_Q5K) {
+        lo[i] |= ((r.c[i] >> (2u * g)) & 0x01010101u) << 4;
+        hi[i] |= ((r.c[i] >> (2u * g + 1u)) & 0x01010101u) << 4;
+      }
+    }
+    float s0, m0, s1, m1;
+    if constexpr (FMT == RTXLLM_FMT_Q4K_RAW || FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE || FMT == RTXLLM_FMT_Q5K) {
+      kq_head_pairs(r.b, g, s0, m0, s1, m1);
+    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
+      s0 = __uint_as_float(r.b[0]), m0 = __uint_as_float(r.b[1]);
+      s1 = __uint_as_float(r.b[2]), m1 = __uint_as_float(r.b[3]);
+    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
+      s0 = h2f(r.b[0]), m0 = h2f(r.b[0] >> 16);
+      s1 = h2f(r.b[1]), m1 = h2f(r.b[1] >> 16);
+    } else {  // split-compact
+      const float d = h2f(r.b[0]), dmin = h2f(r.b[0] >> 16);
+      s0 = d * static_cast<float>(r.b[1] & 0xFFu), s1 = d * static_cast<float>(r.b[1] >> 8);
+      m0 = dmin * static_cast<float>(r.b[2] & 0xFFu), m1 = dmin * static_cast<float>(r.b[2] >> 8);
+    }
+    const float c0 = static_cast<float>(dot16(lo, x0));
+    const float c1 = static_cast<float>(dot16(hi, x1));
+    return ((s0 * x0.s) * c0 - m0 * x0.sum) + ((s1 * x1.s) * c1 - m1 * x1.sum);
+  }
+}
+
+// ---- tile reduction -----------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i -> 7 - i within 8
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor2 = 0x122;
+constexpr int kDppRowRor1 = 0x121;
+
+// v_permlane32_swap / v_permlane16_swap (gfx950): exchange a's upper 32 (odd
+// 16-lane rows') lanes with b's lower 32 (even rows') lanes. Issued as inline
+// asm: this compiler's __builtin_amdgcn_permlane{16,32}_swap treats the two
+// results as one value (it emitted a + a for the sum of both), so the builtin
+// is not usable. The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// acc[j] holds lane partials of row j (T in {4, 8}); afterwards every lane of
+// [r * 64/T, (r+1) * 64/T) holds the full sum of row r. permlane swaps handle
+// lane bits 5 and 4, DPP the bits within 16-lane rows: 8 VALU ops for T = 4.
+template <int T>
+__device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane) {
+  static_assert(T == 4 || T == 8, "tile of 4 or 8 rows");
+#pragma unroll
+  for (int j = 0; j < T / 2; ++j) {
+    float a = acc[j], b = acc[j + T / 2];
+    permlane32_swap(a, b);
+    acc[j] = a + b;
+  }
+#pragma unroll
+  for (int j = 0; j < T / 4; ++j) {
+    float a = acc[j], b = acc[j + T / 4];
+    permlane16_swap(a, b);
+    acc[j] = a + b;
+  }
+  float v = acc[0];
+  if constexpr (T == 8) {
+    // lane bit 3: keep row 0 or 1 of the pair, send the other across ror 8
+    const bool up = (lane & 8u) != 0u;
+    const float keep = up ? acc[1] : acc[0];
+    const float send = up ? acc[0] : acc[1];
+    v = keep + dpp<kDppRowRor8>(send);
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppQuadXor1>(v);
+  } else {
+    v += dpp<kDppRowRor8>(v);
+    v += dpp<kDppRowRor4>(v);
+    v += dpp<kDppRowRor2>(v);
+    v += dpp<kDppRowRor1>(v);
+  }
+  return v;
+}
+
+// ---- the kernel -------------------------------------------------------------
+
+constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slots)
+
+// UPL units (32 columns each) per lane; a row's `cols / 32` units are split over
+// ks waves of one workgroup, which also holds nrg row groups (blockDim.x = 64 *
+// ks * nrg, ks * nrg <= 8). Row group rg of workgroup b handles tiles b + G *
+// (rg + nrg * j), j = 0, 1, ... (G = gridDim.x), so tiles spread evenly over
+// the CUs, and loads the next tile's rows before it computes the current one.
+template <int FMT, int UPL, int TILE, bool SELF, class Epi>
+__global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows, std::uint32_t ks,
+                                                  Epi epi) {
+  // Column-split partials, one slot per wave, double buffered by round parity
+  // so a fast wave cannot overwrite a slot another wave still reads.
+  __shared__ float part[2][kMaxKs][TILE];
+  const std::uint32_t lane = threadIdx.x & 63u;
+  // Wave-uniform values live in SGPRs: row bases become scalar and every load
+  // is (scalar row base + per-lane offset).
+  const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const std::uint32_t kw = wave % ks, rg = wave / ks, nrg = (blockDim.x >> 6) / ks;
+  const std::uint32_t units = w.cols >> 5, bpr = w.cols >> 8;
+
+  std::uint32_t uk[UPL];
+  UnitOff off[UPL];
+  XG x0[UPL], x1[UPL];
+#pragma unroll
+  for (int i = 0; i < UPL; ++i) {
+    std::uint32_t u = (kw * UPL + i) * 64u + lane;
+    const bool valid = u < units;
+    u = valid ? u : units - 1u;
+    const std::uint32_t ub = u >> 3;
+    uk[i] = u & 7u;
+    off[i] = unit_offsets<FMT>(ub, uk[i]);
+    std::uint32_t g0, g1;
+    unit_groups<FMT>(ub, uk[i], g0, g1);
+    if constexpr (SELF) {
+      xg_stage(xs.x, nullptr, g0, x0[i]);
+      xg_stage(xs.x, nullptr, g1, x1[i]);
+    } else {
+      xg_load(xs.xq, g0, x0[i]);
+      xg_load(xs.xq, g1, x1[i]);
+    }
+    if (!valid) {
+      xg_zero(x0[i]);
+      xg_zero(x1[i]);
+    }
+  }
+  const IqLds* tables = nullptr;
+  if constexpr (fmt_is_iq(FMT)) {
+    IqLds& t = iq_lds<FMT>();
+    iq_lds_build<FMT>(t);
+    __syncthreads();
+    tables = &t;
+  }
+
+  const std::size_t prow = static_cast<std::size_t>(bpr) * FmtBytes<FMT>::payload;
+  const std::size_t mrow = static_cast<std::size_t>(bpr) * FmtBytes<FMT>::meta;
+  const std::uint32_t tiles = (rows + TILE - 1) / TILE;
+  const std::uint32_t per_round = gridDim.x * nrg;
+  const std::uint32_t rounds = (tiles + per_round - 1) / per_round;
+
+  auto load_tile = [&](std::uint32_t t, UnitRaw (&raw)[TILE][UPL]) {
+    if (t >= tiles) return;
+#pragma unroll
+    for (int rr = 0; rr < TILE; ++rr) {
+      std::uint32_t row = t * TILE + rr;
+      row = row < rows ? row : rows - 1u;
+#pragma unroll
+      for (int i = 0; i < UPL; ++i) unit_load<FMT>(w.payload + row * prow, w.meta + row * mrow, off[i], raw[rr][i]);
+    }
+  };
+  auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, const UnitRaw (&raw)[TILE][UPL]) {
+    // Every wave of the workgroup runs the same rounds, so the barrier below is
+    // uniform; waves without a tile this round still take part in it.
+    const bool active = t < tiles;
+    float acc[TILE];
+#pragma unroll
+    for (int rr = 0; rr < TILE; ++rr) {
+      acc[rr] = 0.0f;
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) acc[rr] += unit_compute<FMT>(raw[rr][i], off[i], uk[i], x0[i], x1[i], tables);
+      }
+    }
+    float v = tile_reduce<TILE>(acc, lane);
+    constexpr std::uint32_t spread = 64u / TILE;
+    const std::uint32_t r = lane / spread;
+    if (ks > 1u) {
+      if ((lane % spread) == 0u) part[parity][wave][r] = v;
+      __syncthreads();
+      if (kw != 0u) return;
+      v = part[parity][wave][r];
+      for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
+    }
+    if (active) epi(t * TILE, v, lane, rows);
+  };
+
+  UnitRaw ra[TILE][UPL], rb[TILE][UPL];
+  std::uint32_t t = rg * gridDim.x + blockIdx.x;
+  load_tile(t, ra);
+  for (std::uint32_t round = 0; round < rounds; round += 2) {
+    load_tile(t + per_round, rb);
+    finish_tile(t, 0u, ra);
+    t += per_round;
+    if (round + 1 >= rounds) break;
+    load_tile(t + per_round, ra);
+    finish_tile(t, 1u, rb);
+    t += per_round;
+  }
+}
+
+// ---- epilogues ---------------------------------------------------------------
+
+// Row r of the tile is in lanes [r * 64/T, (r+1) * 64/T); epilogues write from the
+// first lane of each range.
+template <int TILE>
+struct EpiStore {
+  float* y;
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane,
+                                             std::uint32_t rows) const {
+    constexpr std::uint32_t spread = 64u / TILE;
+    const std::uint32_t row = row0 + lane / spread;
+    if ((lane % spread) == 0u && row < rows) y[row] = v;
+  }
+};
+
+// The reference's decode side effect (decode_kernels.cu:1600-1606): kv[(row *
+// page_words + (token + row) % page_words) % kv_words] = y[row] for row <
+// active_pages.
+template <int TILE>
+struct EpiDecode {
+  float* y;
+  float* kv;
+  const std::uint32_t* token;
+  std::uint32_t kv_words, page_words, active_pages;
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane,
+                                             std::uint32_t rows) const {
+    constexpr std::uint32_t spread = 64u / TILE;
+    const std::uint32_t row = row0 + lane / spread;
+    if ((lane % spread) != 0u || row >= rows) return;
+    y[row] = v;
+    if (kv != nullptr && row < active_pages && kv_words > 0u && page_words > 0u) {
+      const std::size_t base = static_cast<std::size_t>(row) * page_words;
+      const std::size_t off = (token[0] + row) % page_words;
+      kv[(base + off) % kv_words] = v;
+    }
+  }
+};
+
+}  // namespace rtxllm

@@ -34,6 +34,8 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_launch_iq3s_matvec_decode_probe": [_P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _U, _S],
     "rtxllm_dequant_f32": [c_int, _P, _P, _U, _U, _P, _S],
     "rtxllm_matvec": [c_int, _P, _P, _P, _P, _U, _U, _S],
+    "rtxllm_stage_activation": [_P, _P, _U, _P, _S],
+    "rtxllm_matvec_xq": [c_int, _P, _P, _P, _P, _U, _U, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",
@@ -58,6 +60,7 @@ for _name in (
 _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_format_payload_block_bytes": (c_uint32, [c_int]),
     "rtxllm_format_meta_block_bytes": (c_uint32, [c_int]),
+    "rtxllm_xq_bytes": (c_size_t, [c_uint32]),
     "rtxllm_q4k_split_pack": (c_int, [c_int, _P, c_size_t, _P, _P]),
     "rtxllm_synth_raw_blocks": (c_int, [c_int, c_uint64, c_size_t, c_float, c_float, _P, c_int]),
     "rtxllm_synth_normal_f32": (c_int, [c_uint64, c_size_t, c_float, c_float, _P, c_int]),

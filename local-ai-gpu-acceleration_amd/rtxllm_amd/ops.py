@@ -64,3 +64,32 @@ def dequant(w: DevicePack) -> torch.Tensor:
     check("rtxllm_dequant_f32", lib().rtxllm_dequant_f32(w.fmt, ptr(w.payload), ptr(w.meta), w.rows, w.cols,
                                                          ptr(out), stream()))
     return out
+
+
+def xq_bytes(cols: int) -> int:
+    return int(lib().rtxllm_xq_bytes(cols))
+
+
+def stage(x: torch.Tensor, weight: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Staged activation buffer (uint8, rtxllm_xq_bytes(cols)) of x (* weight)."""
+    cols = x.numel()
+    _check_vec(x, cols)
+    if weight is not None:
+        _check_vec(weight, cols)
+    if out is None:
+        out = torch.empty(xq_bytes(cols), dtype=torch.uint8, device=x.device)
+    if out.numel() < xq_bytes(cols):
+        raise ValueError("staging buffer too small")
+    check("rtxllm_stage_activation", lib().rtxllm_stage_activation(ptr(x), ptr(weight), cols, ptr(out), stream()))
+    return out
+
+
+def matvec_xq(w: DevicePack, xq: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    if xq.dtype != torch.uint8 or xq.numel() < xq_bytes(w.cols) or not xq.is_cuda:
+        raise ValueError("expected a device staging buffer of rtxllm_xq_bytes(cols) bytes")
+    if y is None:
+        y = torch.empty(w.rows, dtype=torch.float32, device=xq.device)
+    _check_vec(y, w.rows)
+    check("rtxllm_matvec_xq", lib().rtxllm_matvec_xq(w.fmt, ptr(w.payload), ptr(w.meta), ptr(xq), ptr(y), w.rows,
+                                                      w.cols, stream()))
+    return y

@@ -49,7 +49,7 @@ def test_dequant_bit_exact(orc, fmt):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(1, 256), (7, 512), (64, 1024), (133, 4096), (37, 2304)])
+@pytest.mark.parametrize("shape", [(1, 256), (7, 512), (64, 1024), (133, 4096), (37, 2304), (2100, 4608)])
 @pytest.mark.parametrize("fmt", ALL_FMTS, ids=[F.NAMES[f] for f in ALL_FMTS])
 def test_matvec_small(orc, fmt, shape):
     rows, cols = shape
@@ -198,3 +198,32 @@ def test_invalid_arguments_rejected():
     assert L.rtxllm_launch_rmsnorm_cache(p(f), p(f), 4, 0, 1e-6, 0, s) == 1
     assert L.rtxllm_launch_rmsnorm_cache_and_gated_product(p(f), p(f), p(f), p(f), 4, 4, 0, 1e-6, 0, s) == 1
     torch.cuda.synchronize()
+
+
+# ---- staged activation + matvec on staged x ------------------------------------
+
+@pytest.mark.parametrize("cols", [256, 4096, 14336])
+def test_stage_bit_exact(orc, cols):
+    x = packs.normal_f32(cols + 5, cols) * np.float32(3.0)
+    w = packs.normal_f32(cols + 6, cols, mean=1.0, std=0.02)
+    for weight in (None, w):
+        got = ops.stage(ops.to_dev(x), None if weight is None else ops.to_dev(weight)).cpu().numpy()
+        ref = orc.stage_bytes(x, weight)
+        assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("shape", [(133, 4096), (512, 14336), (64, 1024)])
+@pytest.mark.parametrize("fmt", ALL_FMTS, ids=[F.NAMES[f] for f in ALL_FMTS])
+def test_matvec_xq_equals_self_staging_and_staged_oracle(orc, fmt, shape):
+    rows, cols = shape
+    pack = packs.make_pack(fmt, rows, cols, seed=5000 + fmt + rows)
+    x = packs.normal_f32(6000 + cols, cols)
+    dev = ops.DevicePack(pack)
+    xd = ops.to_dev(x)
+    y_self = ops.matvec(dev, xd).cpu().numpy()
+    y_xq = ops.matvec_xq(dev, ops.stage(xd)).cpu().numpy()
+    assert np.array_equal(y_self.view(np.uint32), y_xq.view(np.uint32))
+    of, pl, mt = oracle_args(pack)
+    ref = orc.matvec_staged_f64(of, pl, mt, x, rows, cols, 8)
+    # same staged digits: only fp32 rounding of the per-group products separates them
+    assert np.max(np.abs(y_xq - ref)) / np.max(np.abs(ref)) < 1e-5
