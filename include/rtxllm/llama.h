@@ -1,0 +1,91 @@
+/* C-ABI of the MI355X Llama decode runner (batch 1): one resident VRAM arena
+ * holding every layer's packs, the fp16 paged KV cache and the workspace; one
+ * decode step = embedding gather, per layer {fused qkv matvec + RoPE + KV
+ * append, split-context GQA attention, o matvec + residual + ffn-norm staging,
+ * fused gate/up matvec + SiLU-gate, down matvec + residual + next-norm
+ * staging}, final norm + LM head + greedy argmax; replayable as one hipGraph.
+ *
+ * No counterpart in the reference: its layer-slice runner
+ * (runtime/apps/mixed_sequence_benchmark_runner/main.cpp:3136-5818) drives
+ * synthetic stages of one Qwen3.6 layer; this runner keeps its structure
+ * (arena upload, launch sequence, graph capture, replay with the token read
+ * back) for a real Llama decode step. All entry points return hipSuccess or a
+ * hipError_t; hipErrorInvalidValue for rejected configurations. */
+#ifndef RTXLLM_LLAMA_H
+#define RTXLLM_LLAMA_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+  uint32_t hidden;     /* model width, % 256 == 0, <= 16384 */
+  uint32_t n_heads;    /* query heads of 128 dims */
+  uint32_t n_kv_heads; /* kv heads (n_heads % n_kv_heads == 0, group <= 8) */
+  uint32_t ffn;        /* FFN width, % 256 == 0 */
+  uint32_t vocab;
+  uint32_t n_layers;
+  uint32_t max_ctx;    /* KV positions per sequence, % page_size == 0 */
+  uint32_t page_size;  /* positions per KV page */
+  float rope_theta;
+  float rms_eps;
+  int fmt_qkv;         /* formats (enum rtxllm_format) of the stacked q|k|v, o, */
+  int fmt_o;           /* interleaved gate/up, down and LM-head tensors; the */
+  int fmt_gate_up;     /* embedding table is Q5_K */
+  int fmt_down;
+  int fmt_lm_head;
+} rtxllm_llama_config;
+
+typedef struct rtxllm_llama rtxllm_llama;
+
+/* Allocate the arena on the current device (one hipMalloc) and set up the
+ * RoPE table, identity KV block tables, token = 0, pos = 0. */
+hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out);
+void rtxllm_llama_destroy(rtxllm_llama* m);
+
+/* Device pointer (and size) of a named region, or NULL. Per layer: "qkv",
+ * "qkv_meta", "o", "o_meta", "gate_up", "gate_up_meta", "down", "down_meta"
+ * (meta regions exist for Q4_K split layouts only), "attn_norm", "ffn_norm",
+ * "k_cache", "v_cache" (fp16 [pages][n_kv][page_size][128]), "block_table"
+ * (int32 [max_ctx / page_size]). Global (layer ignored): "embed", "lm_head",
+ * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos".
+ * Row layouts: qkv = q rows (n_heads*128) | k rows | v rows; gate_up rows
+ * interleaved (2i = gate_i, 2i+1 = up_i). */
+void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes);
+
+/* Synchronous host <-> region copies (setup and inspection; not capture-safe):
+ * `bytes` at byte `offset` of the region. hipErrorInvalidValue if out of range. */
+hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset, const void* src,
+                               size_t bytes);
+hipError_t rtxllm_llama_download(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset, void* dst,
+                                 size_t bytes);
+
+/* Fill every weight tensor with the seeded synthetic generator (on the device,
+ * bit-identical to rtxllm_synth_raw_blocks): tensor seed = seed + 4096 *
+ * (layer + 1) + role (qkv 1, o 2, gate_up 3, down 4), embed seed + 5, LM head
+ * seed + 6; d, dmin = fp16(U[1e-4, 2e-3]). Norm weights and the KV cache are
+ * left to the caller. Q4_K split layouts other than split-native are refused. */
+hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_t stream);
+
+enum { RTXLLM_LLAMA_EMBED = 1, RTXLLM_LLAMA_HEAD = 2 };
+
+/* Layers [first, last) at position *pos. flags & EMBED: h = embed[*token], else
+ * h is taken as is. flags & HEAD: final norm, LM head, token = argmax, pos += 1. */
+hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint32_t last, int flags, hipStream_t stream);
+/* One full decode step: forward(0, n_layers, EMBED | HEAD). */
+hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream);
+/* Capture one decode step into the model's hipGraph / replay it. */
+hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream);
+hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream);
+/* Kernel launches per decode step. */
+uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,87 @@
+// Host-side interface of the Llama decode-layer kernels (layer.hip), used by the
+// decode runner (model.cpp). All pointers are device pointers; every launcher
+// is asynchronous on `stream` and capture-safe.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rtxllm {
+
+// fp16 paged KV cache of one layer: page p (physical) holds K (and V) as
+// [n_kv_heads][page_size][head_dim]; block_table maps logical page -> physical.
+struct KvLayer {
+  std::uint16_t* k;
+  std::uint16_t* v;
+  const std::int32_t* block_table;
+  std::uint32_t page_size;
+  std::uint32_t n_kv;
+  std::uint32_t capacity;  // positions; a position >= capacity is never read or written
+};
+
+// RMSNorm input of a fused matvec: the staged vector holds h * w (16-value
+// groups), and the matvec multiplies its row sums by 1 / sqrt(sum(h^2) / n +
+// eps), sum(h^2) being the sum of `nslots` partials written by the producer.
+struct NormIn {
+  const void* xq;
+  const float* sumsq;
+  std::uint32_t nslots;
+  std::uint32_t n;
+  float eps;
+};
+
+constexpr std::uint32_t kHeadDim = 128;
+
+// h = dequant(embed[*token]) (Q5_K row, bit-exact; table null: h as is), then
+// xq = stage(h * wnorm), sumsq[0] = sum(h^2), sumsq[1, nslots) = 0.
+// cols % 256 == 0, cols <= 16384; a token >= vocab reads row vocab - 1.
+hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::uint32_t vocab,
+                            const std::uint32_t* token, float* h, const float* wnorm, void* xq, float* sumsq,
+                            std::uint32_t nslots, hipStream_t stream);
+
+// qkv = Wqkv * rmsnorm(h) (q_rows + 2 kv_rows rows, q | k | v), then RoPE (theta
+// schedule inv_freq[head_dim / 2], adjacent pairs) on q and k at position *pos,
+// q -> q_out (fp32), k and v -> fp16 KV cache slot *pos.
+hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
+                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float* inv_freq,
+                      const std::uint32_t* pos, float* q_out, const KvLayer& kv, hipStream_t stream);
+
+// GQA decode attention over positions [0, *pos] of the paged cache: split over
+// context chunks (partials) then combined into att[n_heads * head_dim].
+hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+                            std::uint32_t max_ctx, float* partials, float* att, hipStream_t stream);
+std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx);
+
+// h += W x (rows % 16 == 0) with x = fp32 x_in staged per wave; then xq_next =
+// stage(h * w_next), sumsq_next[t] = sum of h^2 over rows [16 t, 16 t + 16).
+hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                           std::uint32_t cols, const float* x_in, float* h, const float* w_next, void* xq_next,
+                           float* sumsq_next, hipStream_t stream);
+
+// Rows interleaved gate / up (row 2i = gate_i, row 2i + 1 = up_i), x =
+// rmsnorm(h): act[i] = silu(gate_i) * up_i.
+hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                          std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream);
+
+// logits = W rmsnorm(h); argkey = max over rows of (ordered(logit) << 32 | ~row)
+// (greedy argmax, lowest index on ties, NaN never wins). argkey must be 0 before.
+hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* argkey,
+                         hipStream_t stream);
+
+// token[0] = argmax from argkey (0 if every logit was NaN); *pos += advance;
+// argkey = 0.
+hipError_t launch_argmax_finalize(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
+                                  std::uint32_t advance, hipStream_t stream);
+
+// Device-side synthetic packs, bit-identical to the host generator
+// (rtxllm_synth_raw_blocks): raw blocks of format 0/5/6/7, or the Q4_K
+// split-native pair (payload + 16 B heads) of synthetic raw Q4_K blocks.
+hipError_t launch_synth_raw(int fmt, std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                            std::uint8_t* out, hipStream_t stream);
+hipError_t launch_synth_q4k_native(std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                                   std::uint8_t* payload, std::uint8_t* meta, hipStream_t stream);
+
+}  // namespace rtxllm

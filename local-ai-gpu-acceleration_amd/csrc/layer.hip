@@ -1,0 +1,492 @@
+// Llama decode-layer kernels for gfx950: the matvec epilogues that fuse RMSNorm
+// scaling, RoPE, the fp16 KV-cache append, SiLU-gate multiply, residual add and
+// next-norm staging into the producing matvec, plus the Q5_K embedding gather,
+// split-context GQA attention and the greedy-token finalisation.
+//
+// The reference runtime has no Llama layer (SURVEY: its feedback kernels are
+// unweighted RMSNorm / SiLU stand-ins, decode_kernels.cu:122-289, and its
+// attention kernels are synthetic windows); the formulas here are the
+// textbook Llama ones, restated on the CPU in oracle/rtxllm_oracle.c, with the
+// reference's pieces where it has them: RMSNorm eps handling and inv-rms
+// (main.cpp:1363-1382), SiLU v / (1 + exp(-v)) (main.cpp:1435-1503), the
+// rotate-pair arithmetic (decode_kernels.cu:327-343) and the lowest-index
+// argmax (decode_kernels.cu:2993-3031).
+#include <cfloat>
+
+#include "dequant.cuh"
+#include "layer.h"
+#include "mv_launch.cuh"
+
+namespace rtxllm {
+namespace {
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 1 / sqrt(sum / n + eps) from the producer's partial sums of squares. Every
+// lane (and every wave of every kernel) adds the partials in the same order, so
+// all consumers see the same value.
+__device__ __forceinline__ float inv_rms(const float* __restrict__ sumsq, std::uint32_t nslots, std::uint32_t n,
+                                         float eps, std::uint32_t lane) {
+  float s = 0.0f;
+  for (std::uint32_t i = lane; i < nslots; i += 64u) s += sumsq[i];
+  s = wave_sum(s);
+  return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
+}
+
+__device__ __forceinline__ float silu(float v) {
+  const float sig = 1.0f / (1.0f + expf(-v));
+  return v * sig;
+}
+
+__device__ __forceinline__ std::size_t kv_offset(const KvLayer& kv, std::uint32_t pos, std::uint32_t head) {
+  const std::uint32_t page = static_cast<std::uint32_t>(kv.block_table[pos / kv.page_size]);
+  const std::uint32_t slot = pos % kv.page_size;
+  return ((static_cast<std::size_t>(page) * kv.n_kv + head) * kv.page_size + slot) * kHeadDim;
+}
+
+__device__ __forceinline__ std::uint16_t f2h(float v) {
+  return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
+}
+
+// ---- epilogues (TILE 4: row r of a tile in lanes [16 r, 16 r + 16)) ---------
+
+struct EpiQkv {
+  static constexpr int kTile = 4;
+  const float* sumsq;
+  std::uint32_t nslots, n;
+  float eps;
+  std::uint32_t q_rows, kv_rows;
+  const float* inv_freq;
+  const std::uint32_t* pos_ptr;
+  float* q;
+  KvLayer kv;
+  float scale;
+  std::uint32_t pos;
+  __device__ __forceinline__ void init(std::uint32_t lane) {
+    scale = inv_rms(sumsq, nslots, n, eps, lane);
+    pos = *pos_ptr;
+  }
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
+    const std::uint32_t row = row0 + (lane >> 4);
+    const float y = v * scale;
+    const float partner = __shfl_xor(y, 16, 64);  // row ^ 1: the other element of a rotary pair
+    if ((lane & 15u) != 0u || row >= rows) return;
+    if (row >= q_rows && pos >= kv.capacity) return;  // no slot for this position
+    if (row < q_rows + kv_rows) {
+      const std::uint32_t d = row & (kHeadDim - 1u);
+      const float angle = static_cast<float>(pos) * inv_freq[d >> 1];
+      const float s = sinf(angle), c = cosf(angle);
+      // (e, o) -> (e c - o s, e s + o c)
+      const float out = (d & 1u) ? (partner * s + y * c) : (y * c - partner * s);
+      if (row < q_rows) {
+        q[row] = out;
+      } else {
+        const std::uint32_t kr = row - q_rows;
+        kv.k[kv_offset(kv, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
+      }
+    } else {
+      const std::uint32_t vr = row - q_rows - kv_rows;
+      kv.v[kv_offset(kv, pos, vr / kHeadDim) + (vr & (kHeadDim - 1u))] = f2h(y);
+    }
+  }
+};
+
+struct EpiGateUp {
+  static constexpr int kTile = 4;
+  const float* sumsq;
+  std::uint32_t nslots, n;
+  float eps;
+  float* act;
+  float scale;
+  __device__ __forceinline__ void init(std::uint32_t lane) { scale = inv_rms(sumsq, nslots, n, eps, lane); }
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
+    const std::uint32_t row = row0 + (lane >> 4);
+    const float y = v * scale;
+    const float up = __shfl_xor(y, 16, 64);
+    if ((lane & 31u) == 0u && row < rows) act[row >> 1] = silu(y) * up;
+  }
+};
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, std::uint32_t row) {
+  if (v != v) return 0ull;           // NaN never wins
+  if (v == 0.0f) v = 0.0f;           // -0 ties with +0 (first index wins)
+  std::uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - row);
+}
+
+struct EpiLogits {
+  static constexpr int kTile = 4;
+  const float* sumsq;
+  std::uint32_t nslots, n;
+  float eps;
+  float* logits;
+  unsigned long long* argkey;
+  float scale;
+  __device__ __forceinline__ void init(std::uint32_t lane) { scale = inv_rms(sumsq, nslots, n, eps, lane); }
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
+    const std::uint32_t row = row0 + (lane >> 4);
+    const float y = v * scale;
+    const bool ok = row < rows;
+    if ((lane & 15u) == 0u && ok) logits[row] = y;
+    unsigned long long key = ok ? argmax_key(y, row) : 0ull;
+    unsigned long long other = __shfl_xor(key, 16, 64);
+    key = other > key ? other : key;
+    other = __shfl_xor(key, 32, 64);
+    key = other > key ? other : key;
+    if (lane == 0u && key != 0ull) atomicMax(argkey, key);
+  }
+};
+
+// TILE 16: row r of the tile in lanes [4 r, 4 r + 4).
+struct EpiResidual {
+  static constexpr int kTile = 16;
+  float* h;
+  const float* w_next;
+  XQOut xq;
+  float* sumsq;
+  __device__ __forceinline__ void init(std::uint32_t) {}
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t) const {
+    const std::uint32_t row = row0 + (lane >> 2);
+    const bool owner = (lane & 3u) == 0u;
+    const float hn = h[row] + v;
+    if (owner) h[row] = hn;
+    const float sq = wave_sum(owner ? hn * hn : 0.0f);
+    // stage the 16-value group h * w_next exactly as quant16 does
+    const float x = w_next != nullptr ? hn * w_next[row] : hn;
+    const float m = wave_max(fabsf(x));
+    const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
+    const float s = m / kXQLimitF;
+    int X = static_cast<int>(rintf(x * inv));
+    X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
+    int H, M, L;
+    xq_digits(X, H, M, L);
+    const int total = wave_sum_i(owner ? X : 0);
+    if (owner) {
+      xq.h[row] = static_cast<std::int8_t>(H);
+      xq.m[row] = static_cast<std::int8_t>(M);
+      xq.l[row] = static_cast<std::int8_t>(L);
+    }
+    if (lane == 0u) {
+      const std::uint32_t t = row0 / kXGroup;
+      xq.s[t] = s;
+      xq.sum[t] = s * static_cast<float>(total);
+      sumsq[t] = sq;
+    }
+  }
+};
+
+// ---- embedding gather ----------------------------------------------------------
+
+// One workgroup, thread g handles values [16 g, 16 g + 16) of the row.
+__global__ __launch_bounds__(1024) void embed_q5k_kernel(const std::uint8_t* __restrict__ table, std::uint32_t cols,
+                                                         std::uint32_t vocab, const std::uint32_t* __restrict__ token,
+                                                         float* __restrict__ h,
+                                                         const float* __restrict__ wnorm, XQOut xq,
+                                                         float* __restrict__ sumsq, std::uint32_t nslots) {
+  __shared__ float part[16];
+  const std::uint32_t g = threadIdx.x, groups = cols / kXGroup;
+  float sq = 0.0f;
+  if (g < groups) {
+    const std::uint32_t c0 = kXGroup * g;
+    float v[16];
+    if (table != nullptr) {
+      const std::size_t row = token[0] < vocab ? token[0] : vocab - 1u;
+      const std::uint8_t* blk = table + (row * (cols / 256u) + c0 / 256u) * 176u;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        v[j] = dequant_value<RTXLLM_FMT_Q5K>(blk, nullptr, (c0 & 255u) + j);
+        h[c0 + j] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = h[c0 + j];
+    }
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      sq += v[j] * v[j];
+      x[j] = wnorm != nullptr ? v[j] * wnorm[c0 + j] : v[j];
+    }
+    XG st;
+    quant16(x, st);
+    xg_store(xq, g, st);
+  }
+  sq = wave_sum(sq);
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  for (std::uint32_t i = threadIdx.x + 1u; i < nslots; i += blockDim.x) sumsq[i] = 0.0f;
+  if (threadIdx.x == 0u) {
+    float s = 0.0f;
+    for (std::uint32_t i = 0; i < blockDim.x / 64u; ++i) s += part[i];
+    sumsq[0] = s;
+  }
+}
+
+// ---- attention -------------------------------------------------------------------
+
+constexpr std::uint32_t kAttnThreads = 256;
+constexpr std::uint32_t kMaxGroup = 8;
+
+__host__ __device__ inline std::uint32_t attn_chunk(std::uint32_t max_ctx, std::uint32_t n_kv) {
+  std::uint32_t want = max_ctx * n_kv / 256u, p = 32u;
+  while (p * 2u <= want && p < 256u) p *= 2u;
+  return p;
+}
+
+// Workgroup (chunk c, kv head g): the `group` query heads of g over positions
+// [c P, (c + 1) P) ∩ [0, pos]: scores (thread = position), chunk softmax
+// (max m, sum l of exp(s - m)) and o = sum_t exp(s_t - m) v_t (thread = dim).
+// Partial record per head: m, l, o[128].
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
+                                                                    std::uint32_t group, const std::uint32_t* pos_ptr,
+                                                                    std::uint32_t chunk, std::uint32_t nchunks,
+                                                                    float* __restrict__ partials) {
+  __shared__ float qs[kMaxGroup][kHeadDim];
+  __shared__ float sc[kMaxGroup][256];
+  __shared__ float red[kMaxGroup][kAttnThreads / 64];
+  __shared__ float mrow[kMaxGroup], lrow[kMaxGroup];
+  const std::uint32_t c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
+  const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
+  const std::uint32_t p0 = c * chunk;
+  float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * group * (kHeadDim + 2u);
+  if (p0 > pos) {  // chunk beyond the context: empty record
+    for (std::uint32_t i = t; i < group * (kHeadDim + 2u); i += blockDim.x) {
+      const std::uint32_t f = i % (kHeadDim + 2u);
+      rec[i] = f == 0u ? -INFINITY : 0.0f;
+    }
+    return;
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
+  for (std::uint32_t i = t; i < group * kHeadDim; i += blockDim.x)
+    qs[i / kHeadDim][i % kHeadDim] = q[(g * group) * kHeadDim + i];
+  __syncthreads();
+  const std::uint32_t npos = (pos - p0 + 1u) < chunk ? (pos - p0 + 1u) : chunk;
+  for (std::uint32_t i = t; i < chunk; i += blockDim.x) {
+    float s[kMaxGroup];
+    for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] = -INFINITY;
+    if (i < npos) {
+      const uint4* kr = reinterpret_cast<const uint4*>(kv.k + kv_offset(kv, p0 + i, g));
+      for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] = 0.0f;
+#pragma unroll 4
+      for (int w = 0; w < 16; ++w) {
+        const uint4 pk = kr[w];
+        const std::uint32_t words[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
+          const int d = 8 * w + 2 * e;
+          for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] += qs[hh][d] * k0 + qs[hh][d + 1] * k1;
+        }
+      }
+      for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] *= scale;
+    }
+    for (std::uint32_t hh = 0; hh < group; ++hh) sc[hh][i] = s[hh];
+  }
+  __syncthreads();
+  // chunk max and exp-sum per head
+  const std::uint32_t wave = t >> 6, lane = t & 63u, nw = blockDim.x >> 6;
+  for (std::uint32_t hh = 0; hh < group; ++hh) {
+    float m = -INFINITY;
+    for (std::uint32_t i = t; i < chunk; i += blockDim.x) m = fmaxf(m, sc[hh][i]);
+    m = wave_max(m);
+    if (lane == 0u) red[hh][wave] = m;
+  }
+  __syncthreads();
+  if (t < group) {
+    float m = red[t][0];
+    for (std::uint32_t i = 1; i < nw; ++i) m = fmaxf(m, red[t][i]);
+    mrow[t] = m;
+  }
+  __syncthreads();
+  for (std::uint32_t hh = 0; hh < group; ++hh) {
+    float l = 0.0f;
+    for (std::uint32_t i = t; i < chunk; i += blockDim.x) {
+      const float p = i < npos ? expf(sc[hh][i] - mrow[hh]) : 0.0f;
+      sc[hh][i] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0u) red[hh][wave] = l;
+  }
+  __syncthreads();
+  if (t < group) {
+    float l = 0.0f;
+    for (std::uint32_t i = 0; i < nw; ++i) l += red[t][i];
+    lrow[t] = l;
+  }
+  __syncthreads();
+  // o[hh][d] = sum_i p[hh][i] v[i][d]
+  for (std::uint32_t o = t; o < group * kHeadDim; o += blockDim.x) {
+    const std::uint32_t hh = o / kHeadDim, d = o % kHeadDim;
+    float acc = 0.0f;
+    for (std::uint32_t i = 0; i < npos; ++i) acc += sc[hh][i] * h2f(kv.v[kv_offset(kv, p0 + i, g) + d]);
+    rec[hh * (kHeadDim + 2u) + 2u + d] = acc;
+  }
+  if (t < group) {
+    rec[t * (kHeadDim + 2u)] = mrow[t];
+    rec[t * (kHeadDim + 2u) + 1u] = lrow[t];
+  }
+}
+
+// One workgroup per query head, thread = dim: merge the chunk records
+// (m_c, l_c, o_c) of its kv head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c.
+__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __restrict__ partials,
+                                                                std::uint32_t group, const std::uint32_t* pos_ptr,
+                                                                std::uint32_t capacity, std::uint32_t chunk,
+                                                                std::uint32_t nchunks, float* __restrict__ att) {
+  const std::uint32_t head = blockIdx.x, d = threadIdx.x;
+  const std::uint32_t g = head / group, hh = head % group;
+  const std::uint32_t pos = *pos_ptr < capacity ? *pos_ptr : capacity - 1u;
+  const std::uint32_t active = pos / chunk + 1u;
+  const std::uint32_t n = active < nchunks ? active : nchunks;
+  const float* base = partials + (static_cast<std::size_t>(g) * nchunks) * group * (kHeadDim + 2u) +
+                      hh * (kHeadDim + 2u);
+  const std::size_t stride = group * (kHeadDim + 2u);
+  float M = -INFINITY;
+  for (std::uint32_t c = 0; c < n; ++c) M = fmaxf(M, base[c * stride]);
+  float L = 0.0f, o = 0.0f;
+  for (std::uint32_t c = 0; c < n; ++c) {
+    const float w = expf(base[c * stride] - M);
+    L += w * base[c * stride + 1u];
+    o += w * base[c * stride + 2u + d];
+  }
+  att[head * kHeadDim + d] = o / L;
+}
+
+__global__ void argmax_finalize_kernel(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
+                                       std::uint32_t advance) {
+  if (threadIdx.x != 0u) return;
+  const unsigned long long key = *argkey;
+  token[0] = key == 0ull ? 0u : 0xFFFFFFFFu - static_cast<std::uint32_t>(key & 0xFFFFFFFFull);
+  if (pos != nullptr) pos[0] += advance;
+  *argkey = 0ull;
+}
+
+// ---- device-side synthetic packs ------------------------------------------------
+
+__global__ void synth_raw_kernel(int fmt, std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                                 std::uint8_t* out) {
+  const std::size_t b = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+  if (b >= n_blocks) return;
+  const std::uint32_t bb = rtxllm_format_payload_bytes(fmt);
+  rtxllm_synth_raw_blocks(fmt, seed, b, 1, d_lo, d_hi, out + b * bb);
+}
+
+__global__ void synth_q4k_native_kernel(std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                                        std::uint8_t* payload, std::uint8_t* meta) {
+  const std::size_t b = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+  if (b >= n_blocks) return;
+  std::uint8_t blk[144];
+  rtxllm_synth_raw_blocks(RTXLLM_FMT_Q4K_RAW, seed, b, 1, d_lo, d_hi, blk);
+  for (int i = 0; i < 16; ++i) meta[b * 16u + i] = blk[i];
+  for (int i = 0; i < 128; ++i) payload[b * 128u + i] = blk[16 + i];
+}
+
+}  // namespace
+
+hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::uint32_t vocab,
+                            const std::uint32_t* token, float* h, const float* wnorm, void* xq, float* sumsq,
+                            std::uint32_t nslots, hipStream_t stream) {
+  if (cols == 0u || (cols % 256u) != 0u || cols > 16384u || nslots == 0u || vocab == 0u) return hipErrorInvalidValue;
+  const std::uint32_t threads = ((cols / kXGroup + 63u) / 64u) * 64u;  // whole waves
+  hipLaunchKernelGGL(embed_q5k_kernel, dim3(1), dim3(threads), 0, stream, table, cols, vocab, token, h, wnorm,
+                     xq_out(xq, cols), sumsq, nslots);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
+                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float* inv_freq,
+                      const std::uint32_t* pos, float* q_out, const KvLayer& kv, hipStream_t stream) {
+  const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
+  EpiQkv e{};
+  e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps;
+  e.q_rows = q_rows, e.kv_rows = kv_rows, e.inv_freq = inv_freq, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, w.rows, e, stream);
+}
+
+std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx) {
+  const std::uint32_t chunk = attn_chunk(max_ctx, n_kv);
+  const std::uint32_t nchunks = (max_ctx + chunk - 1u) / chunk;
+  return static_cast<std::size_t>(n_kv) * nchunks * (n_heads / n_kv) * (kHeadDim + 2u);
+}
+
+hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+                            std::uint32_t max_ctx, float* partials, float* att, hipStream_t stream) {
+  if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
+      kv.capacity > max_ctx)
+    return hipErrorInvalidValue;
+  const std::uint32_t group = n_heads / kv.n_kv;
+  const std::uint32_t chunk = attn_chunk(max_ctx, kv.n_kv);
+  const std::uint32_t nchunks = (max_ctx + chunk - 1u) / chunk;
+  hipLaunchKernelGGL(attn_partial_kernel, dim3(nchunks, kv.n_kv), dim3(kAttnThreads), 0, stream, q, kv, group, pos,
+                     chunk, nchunks, partials);
+  hipError_t st = hipGetLastError();
+  if (st != hipSuccess) return st;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(kHeadDim), 0, stream, partials, group, pos,
+                     kv.capacity, chunk, nchunks, att);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                           std::uint32_t cols, const float* x_in, float* h, const float* w_next, void* xq_next,
+                           float* sumsq_next, hipStream_t stream) {
+  if ((rows % kXGroup) != 0u) return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  const EpiResidual e{h, w_next, xq_out(xq_next, rows), sumsq_next};
+  return launch_mv<true>(fmt, w, XSrc{XQ{}, x_in}, rows, e, stream);
+}
+
+hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                          std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream) {
+  if ((rows % 4u) != 0u) return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  EpiGateUp e{};
+  e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.act = act;
+  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
+}
+
+hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* argkey,
+                         hipStream_t stream) {
+  const QTensor w{payload, meta, rows, cols};
+  EpiLogits e{};
+  e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.logits = logits, e.argkey = argkey;
+  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
+}
+
+hipError_t launch_argmax_finalize(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
+                                  std::uint32_t advance, hipStream_t stream) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(64), 0, stream, argkey, token, pos, advance);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_raw(int fmt, std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                            std::uint8_t* out, hipStream_t stream) {
+  if (fmt != RTXLLM_FMT_Q4K_RAW && fmt != RTXLLM_FMT_Q5K && fmt != RTXLLM_FMT_IQ2S && fmt != RTXLLM_FMT_IQ3S)
+    return hipErrorInvalidValue;
+  if (n_blocks == 0u) return hipSuccess;
+  hipLaunchKernelGGL(synth_raw_kernel, dim3(static_cast<unsigned>((n_blocks + 255u) / 256u)), dim3(256), 0, stream,
+                     fmt, seed, n_blocks, d_lo, d_hi, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_q4k_native(std::uint64_t seed, std::size_t n_blocks, float d_lo, float d_hi,
+                                   std::uint8_t* payload, std::uint8_t* meta, hipStream_t stream) {
+  if (n_blocks == 0u) return hipSuccess;
+  hipLaunchKernelGGL(synth_q4k_native_kernel, dim3(static_cast<unsigned>((n_blocks + 255u) / 256u)), dim3(256), 0,
+                     stream, seed, n_blocks, d_lo, d_hi, payload, meta);
+  return hipGetLastError();
+}
+
+}  // namespace rtxllm

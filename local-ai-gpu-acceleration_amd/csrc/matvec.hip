@@ -2,84 +2,13 @@
 #include "rtxllm/decode_kernels.h"
 
 #include "internal.h"
-#include "mv.cuh"
+#include "dequant.cuh"
+#include "mv_launch.cuh"
 
 namespace rtxllm {
 namespace {
 
 constexpr int kTile = 4;
-
-[[maybe_unused]] int num_cus() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cached = n;
-    else
-      cached = 256;
-  }
-  return cached;
-}
-
-// Launch geometry of mv_kernel, from a sweep on MI355X at the 8B shapes: one
-// unit (32 columns) per lane for rows of up to 16384 columns (two beyond),
-// ks = ceil(units / 64) waves per row, nrg = 4 / ks row groups per workgroup
-// (at least 1), and one 4-row tile per row group: many small workgroups keep
-// enough loads in flight and the dispatcher's tail short.
-struct MvGeom {
-  int upl;
-  unsigned ks, nrg, grid;
-};
-
-bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, MvGeom& g) {
-  (void)fmt;
-  const std::uint32_t units = cols / 32u;
-  g.upl = units > 512u ? 2 : 1;
-  g.ks = (units + 64u * g.upl - 1u) / (64u * g.upl);
-  if (g.ks > static_cast<unsigned>(kMaxKs)) return false;
-  g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
-  const std::uint32_t tiles = (rows + tile - 1) / tile;
-  const std::uint32_t grid = (tiles + g.nrg - 1) / g.nrg;
-  g.grid = grid < 1u ? 1u : (grid > 1048576u ? 1048576u : grid);
-  return true;
-}
-
-template <int FMT, bool SELF, class Epi>
-hipError_t launch_mv_fmt(const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
-                         hipStream_t stream) {
-  MvGeom g;
-  if (!mv_geom(FMT, row_count, w.cols, kTile, g)) return hipErrorInvalidValue;
-  const dim3 grid(g.grid), block(64u * g.ks * g.nrg);
-  if (g.upl == 2) {
-    hipLaunchKernelGGL((mv_kernel<FMT, 2, kTile, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
-  } else {
-    hipLaunchKernelGGL((mv_kernel<FMT, 1, kTile, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
-  }
-  return hipGetLastError();
-}
-
-template <bool SELF, class Epi>
-hipError_t launch_mv(int fmt, const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
-                     hipStream_t stream) {
-  switch (fmt) {
-    case RTXLLM_FMT_Q4K_RAW: return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q4K_SPLIT_PREDECODED:
-      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_PREDECODED, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q4K_SPLIT_HALF:
-      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_HALF, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q4K_SPLIT_COMPACT:
-      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_COMPACT, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
-      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q5K: return launch_mv_fmt<RTXLLM_FMT_Q5K, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_IQ2S: return launch_mv_fmt<RTXLLM_FMT_IQ2S, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_IQ3S: return launch_mv_fmt<RTXLLM_FMT_IQ3S, SELF>(w, xs, row_count, epi, stream);
-    case RTXLLM_FMT_Q4K_RAW_PREDECODED:
-      return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED, SELF>(w, xs, row_count, epi, stream);
-    default: return hipErrorInvalidValue;
-  }
-}
 
 bool needs_meta(int fmt) { return rtxllm_format_meta_bytes(fmt) != 0u; }
 
@@ -100,68 +29,6 @@ bool pointers_ok(int fmt, const void* payload, const void* meta, const void* x) 
 
 // ---- bit-exact dequant -----------------------------------------------------
 
-#pragma clang fp contract(off)
-// Value v of a block, with the reference's expression order (main.cpp:1133-1259).
-template <int FMT>
-__device__ float dequant_value(const std::uint8_t* p, const std::uint8_t* m, std::uint32_t v) {
-  if constexpr (FMT == RTXLLM_FMT_Q5K) {
-    const float d = f16_bits_to_f32(ld_u16(p));
-    const float dmin = f16_bits_to_f32(ld_u16(p + 2));
-    const std::uint32_t g = v >> 6, lane = v & 31u, high = (v & 63u) >= 32u;
-    std::uint32_t sc, mn;
-    scale_min_k4(static_cast<int>(2u * g + high), ld_u32(p + 4), ld_u32(p + 8), ld_u32(p + 12), sc, mn);
-    const std::uint32_t packed = p[48u + 32u * g + lane];
-    const std::uint32_t low = high ? (packed >> 4) : (packed & 15u);
-    const std::uint32_t quant = low + (((p[16u + lane] >> (2u * g + high)) & 1u) ? 16u : 0u);
-    return d * static_cast<float>(sc) * static_cast<float>(quant) - dmin * static_cast<float>(mn);
-  } else if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    const std::uint32_t ib32 = v >> 5, grp = (v & 31u) >> 3, lane = v & 7u;
-    const float d = f16_bits_to_f32(ld_u16(p));
-    const std::uint32_t go = ib32 * 4u + grp;
-    const std::uint32_t idx = p[2u + go] | ((static_cast<std::uint32_t>(p[66u + ib32]) << (8u - 2u * grp)) & 0x300u);
-    const std::uint32_t grid = 2u * ((kIq2sGridDev[idx] >> (2u * lane)) & 3u) + 1u;
-    const std::uint32_t sb = p[74u + ib32];
-    const std::uint32_t nib = grp < 2u ? (sb & 15u) : (sb >> 4);
-    const float scale = d * (0.5f + static_cast<float>(nib)) * 0.25f;
-    const bool neg = (p[34u + go] >> lane) & 1u;
-    return scale * static_cast<float>(grid) * (neg ? -1.0f : 1.0f);
-  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    const std::uint32_t ib32 = v >> 5, grp = (v & 31u) >> 3, lane = v & 7u, pair = lane >> 2, gl = lane & 3u;
-    const float d = f16_bits_to_f32(ld_u16(p));
-    const std::uint32_t sel = ib32 * 8u + grp * 2u + pair;
-    const std::uint32_t hb = (p[66u + ib32] >> (2u * grp + pair)) & 1u;
-    const std::uint32_t idx = p[2u + sel] | (hb << 8);
-    const std::uint32_t grid = (kIq3sGridDev[idx] >> (8u * gl)) & 0xFFu;
-    const std::uint32_t sb = p[106u + (ib32 >> 1)];
-    const std::uint32_t nib = (ib32 & 1u) == 0u ? (sb & 15u) : (sb >> 4);
-    const float scale = d * static_cast<float>(1u + 2u * nib);
-    const bool neg = (p[74u + ib32 * 4u + grp] >> lane) & 1u;
-    return scale * static_cast<float>(grid) * (neg ? -1.0f : 1.0f);
-  } else {
-    const std::uint32_t g = v >> 6, lane = v & 31u, high = (v & 63u) >= 32u, pair = 2u * g + high;
-    const std::uint8_t* qs = (FMT == RTXLLM_FMT_Q4K_RAW || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) ? p + 16 : p;
-    const std::uint32_t packed = qs[32u * g + lane];
-    const float quant = static_cast<float>(high ? (packed >> 4) : (packed & 15u));
-    if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
-      const float* pm = reinterpret_cast<const float*>(m) + 2u * pair;
-      return pm[0] * quant - pm[1];
-    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
-      return f16_bits_to_f32(ld_u16(m + 4u * pair)) * quant - f16_bits_to_f32(ld_u16(m + 4u * pair + 2u));
-    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_COMPACT) {
-      const float d = f16_bits_to_f32(ld_u16(m));
-      const float dmin = f16_bits_to_f32(ld_u16(m + 2));
-      return d * static_cast<float>(m[4u + pair]) * quant - dmin * static_cast<float>(m[12u + pair]);
-    } else {  // native head: split-native metadata or the raw block itself
-      const std::uint8_t* h = (FMT == RTXLLM_FMT_Q4K_RAW) ? p : m;
-      const float d = f16_bits_to_f32(ld_u16(h));
-      const float dmin = f16_bits_to_f32(ld_u16(h + 2));
-      std::uint32_t sc, mn;
-      scale_min_k4(static_cast<int>(pair), ld_u32(h + 4), ld_u32(h + 8), ld_u32(h + 12), sc, mn);
-      return d * static_cast<float>(sc) * quant - dmin * static_cast<float>(mn);
-    }
-  }
-}
-#pragma clang fp contract(on)
 
 // One workgroup of 256 threads per block; thread v writes value v.
 template <int FMT>

@@ -1,0 +1,307 @@
+// Llama decode runner (batch 1) on one MI355X: arena layout, synthetic weight
+// fill, the per-step launch sequence and its hipGraph.
+//
+// Structure follows the reference's layer-slice runner
+// (runtime/apps/mixed_sequence_benchmark_runner/main.cpp: arena setup
+// 3764-3791, per-stage launches 4002-4279, capture 4801-4823, replay
+// 4825-4836), for a real Llama layer instead of its synthetic stages.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "layer.h"
+#include "rtxllm/decode_kernels.h"
+#include "rtxllm/hip_graph_bucket.h"
+#include "rtxllm/llama.h"
+#include "rtxllm/vram_arena.h"
+#include "synth.h"
+#include "xq.h"
+
+struct rtxllm_llama {
+  rtxllm_llama_config cfg{};
+  rtxllm::VramSuperallocator arena;
+  rtxllm::HipGraphBucket graph;
+  std::uint32_t q_rows = 0, kv_rows = 0, nslots = 0;
+  std::size_t partial_floats = 0;
+};
+
+namespace {
+
+using rtxllm::ArenaSpec;
+
+std::size_t blocks_of(std::uint32_t rows, std::uint32_t cols) {
+  return static_cast<std::size_t>(rows) * (cols / 256u);
+}
+
+bool format_ok(int fmt) {
+  return fmt >= RTXLLM_FMT_Q4K_RAW && fmt < RTXLLM_FMT_COUNT;
+}
+
+std::string layer_name(const char* role, std::uint32_t layer) {
+  return "L" + std::to_string(layer) + "." + role;
+}
+
+// Payload and (for Q4_K split layouts) metadata regions of one weight tensor.
+void add_tensor(std::vector<ArenaSpec>& specs, const std::string& name, int fmt, std::uint32_t rows,
+                std::uint32_t cols) {
+  const std::size_t nb = blocks_of(rows, cols);
+  specs.push_back({name, nb * rtxllm_format_payload_bytes(fmt)});
+  if (rtxllm_format_meta_bytes(fmt) != 0u) specs.push_back({name + "_meta", nb * rtxllm_format_meta_bytes(fmt)});
+}
+
+struct TensorRef {
+  const std::uint8_t* payload;
+  const std::uint8_t* meta;
+};
+
+TensorRef tensor(const rtxllm_llama* m, const std::string& name) {
+  const auto* base = static_cast<const std::uint8_t*>(m->arena.arena_ptr(name));
+  const std::uint8_t* meta =
+      m->arena.has_arena(name + "_meta") ? static_cast<const std::uint8_t*>(m->arena.arena_ptr(name + "_meta")) : nullptr;
+  return {base, meta};
+}
+
+template <class T>
+T* region(const rtxllm_llama* m, const std::string& name) {
+  return static_cast<T*>(m->arena.arena_ptr(name));
+}
+
+rtxllm::KvLayer kv_layer(const rtxllm_llama* m, std::uint32_t layer) {
+  rtxllm::KvLayer kv{};
+  kv.k = region<std::uint16_t>(m, layer_name("k_cache", layer));
+  kv.v = region<std::uint16_t>(m, layer_name("v_cache", layer));
+  kv.block_table = region<std::int32_t>(m, layer_name("block_table", layer));
+  kv.page_size = m->cfg.page_size;
+  kv.n_kv = m->cfg.n_kv_heads;
+  kv.capacity = m->cfg.max_ctx;
+  return kv;
+}
+
+hipError_t synth_tensor(rtxllm_llama* m, const std::string& name, int fmt, std::uint32_t rows, std::uint32_t cols,
+                        std::uint64_t seed, hipStream_t stream) {
+  const std::size_t nb = blocks_of(rows, cols);
+  auto* dst = region<std::uint8_t>(m, name);
+  constexpr float kLo = 1e-4f, kHi = 2e-3f;
+  if (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE)
+    return rtxllm::launch_synth_q4k_native(seed, nb, kLo, kHi, dst, region<std::uint8_t>(m, name + "_meta"), stream);
+  if (rtxllm_format_meta_bytes(fmt) != 0u) return hipErrorInvalidValue;
+  return rtxllm::launch_synth_raw(fmt, seed, nb, kLo, kHi, dst, stream);
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out) {
+  if (cfg == nullptr || out == nullptr) return hipErrorInvalidValue;
+  *out = nullptr;
+  const rtxllm_llama_config& c = *cfg;
+  const bool shapes_ok = c.hidden != 0u && c.hidden % 256u == 0u && c.hidden <= 16384u && c.n_heads != 0u &&
+                         c.n_kv_heads != 0u && c.n_heads % c.n_kv_heads == 0u && c.n_heads / c.n_kv_heads <= 8u &&
+                         (c.n_heads * rtxllm::kHeadDim) % 256u == 0u && c.ffn != 0u && c.ffn % 256u == 0u &&
+                         c.vocab != 0u && c.n_layers != 0u && c.page_size != 0u && c.max_ctx != 0u &&
+                         c.max_ctx % c.page_size == 0u && c.rms_eps >= 0.0f && c.rope_theta > 0.0f;
+  if (!shapes_ok || !format_ok(c.fmt_qkv) || !format_ok(c.fmt_o) || !format_ok(c.fmt_gate_up) ||
+      !format_ok(c.fmt_down) || !format_ok(c.fmt_lm_head))
+    return hipErrorInvalidValue;
+
+  std::unique_ptr<rtxllm_llama> m(new (std::nothrow) rtxllm_llama());
+  if (!m) return hipErrorOutOfMemory;
+  m->cfg = c;
+  m->q_rows = c.n_heads * rtxllm::kHeadDim;
+  m->kv_rows = c.n_kv_heads * rtxllm::kHeadDim;
+  m->nslots = c.hidden / rtxllm::kXGroup;
+  m->partial_floats = rtxllm::attention_partials_floats(c.n_heads, c.n_kv_heads, c.max_ctx);
+
+  const std::size_t kv_halves =
+      static_cast<std::size_t>(c.max_ctx / c.page_size) * c.n_kv_heads * c.page_size * rtxllm::kHeadDim;
+  std::vector<ArenaSpec> specs;
+  for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+    add_tensor(specs, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden);
+    add_tensor(specs, layer_name("o", l), c.fmt_o, c.hidden, m->q_rows);
+    add_tensor(specs, layer_name("gate_up", l), c.fmt_gate_up, 2u * c.ffn, c.hidden);
+    add_tensor(specs, layer_name("down", l), c.fmt_down, c.hidden, c.ffn);
+    specs.push_back({layer_name("attn_norm", l), 4u * c.hidden});
+    specs.push_back({layer_name("ffn_norm", l), 4u * c.hidden});
+    specs.push_back({layer_name("k_cache", l), 2u * kv_halves});
+    specs.push_back({layer_name("v_cache", l), 2u * kv_halves});
+    specs.push_back({layer_name("block_table", l), 4u * (c.max_ctx / c.page_size)});
+  }
+  specs.push_back({"embed", blocks_of(c.vocab, c.hidden) * 176u});
+  add_tensor(specs, "lm_head", c.fmt_lm_head, c.vocab, c.hidden);
+  specs.push_back({"out_norm", 4u * c.hidden});
+  specs.push_back({"h", 4u * c.hidden});
+  specs.push_back({"xq", rtxllm::xq_bytes(c.hidden)});
+  specs.push_back({"sumsq", 4u * m->nslots});
+  specs.push_back({"q", 4u * m->q_rows});
+  specs.push_back({"att", 4u * m->q_rows});
+  specs.push_back({"attn_partials", 4u * m->partial_floats});
+  specs.push_back({"act", 4u * c.ffn});
+  specs.push_back({"logits", 4u * c.vocab});
+  specs.push_back({"argkey", 8u});
+  specs.push_back({"token", 4u});
+  specs.push_back({"pos", 4u});
+  specs.push_back({"inv_freq", 4u * rtxllm::kHeadDim / 2u});
+  try {
+    m->arena.initialize(specs);
+    m->arena.reset();
+  } catch (const std::exception&) {
+    return hipErrorOutOfMemory;
+  }
+
+  // RoPE frequencies theta^(-2i/d), computed in double and rounded once; identity block tables.
+  std::vector<float> inv_freq(rtxllm::kHeadDim / 2u);
+  for (std::uint32_t i = 0; i < inv_freq.size(); ++i)
+    inv_freq[i] = static_cast<float>(std::pow(static_cast<double>(c.rope_theta),
+                                              -2.0 * static_cast<double>(i) / static_cast<double>(rtxllm::kHeadDim)));
+  hipError_t st = hipMemcpy(m->arena.arena_ptr("inv_freq"), inv_freq.data(), 4u * inv_freq.size(), hipMemcpyHostToDevice);
+  if (st != hipSuccess) return st;
+  std::vector<std::int32_t> table(c.max_ctx / c.page_size);
+  for (std::uint32_t i = 0; i < table.size(); ++i) table[i] = static_cast<std::int32_t>(i);
+  for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+    st = hipMemcpy(m->arena.arena_ptr(layer_name("block_table", l)), table.data(), 4u * table.size(),
+                   hipMemcpyHostToDevice);
+    if (st != hipSuccess) return st;
+  }
+  *out = m.release();
+  return hipSuccess;
+}
+
+extern "C" void rtxllm_llama_destroy(rtxllm_llama* m) { delete m; }
+
+extern "C" void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes) {
+  if (m == nullptr || name == nullptr) return nullptr;
+  static const char* kPerLayer[] = {"qkv", "qkv_meta", "o", "o_meta", "gate_up", "gate_up_meta", "down",
+                                    "down_meta", "attn_norm", "ffn_norm", "k_cache", "v_cache", "block_table"};
+  std::string key = name;
+  for (const char* p : kPerLayer)
+    if (key == p) {
+      if (layer >= m->cfg.n_layers) return nullptr;
+      key = layer_name(name, layer);
+      break;
+    }
+  if (!m->arena.has_arena(key)) return nullptr;
+  const rtxllm::ArenaView v = m->arena.arena(key);
+  if (bytes != nullptr) *bytes = v.bytes;
+  return static_cast<std::uint8_t*>(m->arena.base()) + v.offset;
+}
+
+extern "C" hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset,
+                                          const void* src, size_t bytes) {
+  std::size_t size = 0;
+  auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
+  if (base == nullptr || src == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
+  return hipMemcpy(base + offset, src, bytes, hipMemcpyHostToDevice);
+}
+
+extern "C" hipError_t rtxllm_llama_download(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset,
+                                            void* dst, size_t bytes) {
+  std::size_t size = 0;
+  auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
+  if (base == nullptr || dst == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
+  return hipMemcpy(dst, base + offset, bytes, hipMemcpyDeviceToHost);
+}
+
+extern "C" hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_t stream) {
+  if (m == nullptr) return hipErrorInvalidValue;
+  const rtxllm_llama_config& c = m->cfg;
+  hipError_t st = hipSuccess;
+  for (std::uint32_t l = 0; l < c.n_layers && st == hipSuccess; ++l) {
+    const std::uint64_t ls = seed + 4096u * (static_cast<std::uint64_t>(l) + 1u);
+    st = synth_tensor(m, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden, ls + 1u, stream);
+    if (st == hipSuccess) st = synth_tensor(m, layer_name("o", l), c.fmt_o, c.hidden, m->q_rows, ls + 2u, stream);
+    if (st == hipSuccess)
+      st = synth_tensor(m, layer_name("gate_up", l), c.fmt_gate_up, 2u * c.ffn, c.hidden, ls + 3u, stream);
+    if (st == hipSuccess) st = synth_tensor(m, layer_name("down", l), c.fmt_down, c.hidden, c.ffn, ls + 4u, stream);
+  }
+  if (st == hipSuccess) st = synth_tensor(m, "embed", RTXLLM_FMT_Q5K, c.vocab, c.hidden, seed + 5u, stream);
+  if (st == hipSuccess) st = synth_tensor(m, "lm_head", c.fmt_lm_head, c.vocab, c.hidden, seed + 6u, stream);
+  return st;
+}
+
+extern "C" hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint32_t last, int flags,
+                                           hipStream_t stream) {
+  if (m == nullptr || first > last || last > m->cfg.n_layers) return hipErrorInvalidValue;
+  const rtxllm_llama_config& c = m->cfg;
+  auto* h = region<float>(m, "h");
+  void* xq = m->arena.arena_ptr("xq");
+  auto* sumsq = region<float>(m, "sumsq");
+  auto* token = region<std::uint32_t>(m, "token");
+  auto* pos = region<std::uint32_t>(m, "pos");
+  const float* first_norm = first < last ? region<float>(m, layer_name("attn_norm", first)) : region<float>(m, "out_norm");
+
+  hipError_t st = rtxllm::launch_embed_q5k((flags & RTXLLM_LLAMA_EMBED) ? region<std::uint8_t>(m, "embed") : nullptr,
+                                           c.hidden, c.vocab, token, h, first_norm, xq, sumsq, m->nslots, stream);
+  const rtxllm::NormIn in{xq, sumsq, m->nslots, c.hidden, c.rms_eps};
+  for (std::uint32_t l = first; l < last && st == hipSuccess; ++l) {
+    const rtxllm::KvLayer kv = kv_layer(m, l);
+    const TensorRef qkv = tensor(m, layer_name("qkv", l));
+    st = rtxllm::launch_qkv(c.fmt_qkv, qkv.payload, qkv.meta, c.hidden, in, m->q_rows, m->kv_rows,
+                            region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv, stream);
+    if (st != hipSuccess) break;
+    st = rtxllm::launch_attention(region<float>(m, "q"), kv, c.n_heads, pos, c.max_ctx,
+                                  region<float>(m, "attn_partials"), region<float>(m, "att"), stream);
+    if (st != hipSuccess) break;
+    const TensorRef o = tensor(m, layer_name("o", l));
+    st = rtxllm::launch_residual(c.fmt_o, o.payload, o.meta, c.hidden, m->q_rows, region<float>(m, "att"), h,
+                                 region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
+    if (st != hipSuccess) break;
+    const TensorRef gu = tensor(m, layer_name("gate_up", l));
+    st = rtxllm::launch_gate_up(c.fmt_gate_up, gu.payload, gu.meta, 2u * c.ffn, c.hidden, in, region<float>(m, "act"),
+                                stream);
+    if (st != hipSuccess) break;
+    const TensorRef dn = tensor(m, layer_name("down", l));
+    const float* next_norm =
+        l + 1u < last ? region<float>(m, layer_name("attn_norm", l + 1u)) : region<float>(m, "out_norm");
+    st = rtxllm::launch_residual(c.fmt_down, dn.payload, dn.meta, c.hidden, c.ffn, region<float>(m, "act"), h,
+                                 next_norm, xq, sumsq, stream);
+  }
+  if (st == hipSuccess && (flags & RTXLLM_LLAMA_HEAD)) {
+    const TensorRef lm = tensor(m, "lm_head");
+    auto* argkey = region<unsigned long long>(m, "argkey");
+    st = rtxllm::launch_logits(c.fmt_lm_head, lm.payload, lm.meta, c.vocab, c.hidden, in, region<float>(m, "logits"),
+                               argkey, stream);
+    if (st == hipSuccess) st = rtxllm::launch_argmax_finalize(argkey, token, pos, 1u, stream);
+  }
+  return st;
+}
+
+extern "C" hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream) {
+  if (m == nullptr) return hipErrorInvalidValue;
+  return rtxllm_llama_forward(m, 0u, m->cfg.n_layers, RTXLLM_LLAMA_EMBED | RTXLLM_LLAMA_HEAD, stream);
+}
+
+extern "C" uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m) {
+  return m == nullptr ? 0u : 1u + 6u * m->cfg.n_layers + 2u;
+}
+
+extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream) {
+  if (m == nullptr || stream == nullptr) return hipErrorInvalidValue;
+  hipError_t st = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+  if (st != hipSuccess) return st;
+  const hipError_t launch = rtxllm_llama_step(m, stream);
+  hipGraph_t g = nullptr;
+  st = hipStreamEndCapture(stream, &g);
+  if (launch != hipSuccess) {
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    return launch;
+  }
+  if (st != hipSuccess) return st;
+  try {
+    m->graph.instantiate(g);
+  } catch (const std::exception&) {
+    return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+extern "C" hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream) {
+  if (m == nullptr || !m->graph.instantiated()) return hipErrorInvalidValue;
+  try {
+    m->graph.replay(stream);
+  } catch (const std::exception&) {
+    return hipErrorLaunchFailure;
+  }
+  return hipSuccess;
+}

@@ -10,8 +10,8 @@
 // the K-quants, coalesced across the 64 lanes) and accumulates
 //   Q4_K/Q5_K:  S_sub * (s_x * sum(q * X)) - M_sub * sum(x_hat)
 //   IQ2_S/3_S:  scale_sub * s_x * sum(+-grid * X)
-// with the integer sums from v_dot4_i32_i8 on int8 weight codes and the int8
-// activation digits. Per-row partial sums of a tile are folded across the 64
+// with the integer sums from v_dot4_i32_i8 on int8 weight codes and the three
+// int8 activation digits (xq.h). Per-row partial sums of a tile are folded across the 64
 // lanes by a butterfly transpose-reduce, which leaves row r of the tile in
 // lanes [r * 64/TILE, (r+1) * 64/TILE); wide rows (cols > 4096) split their
 // columns over KS waves of one workgroup and add the KS partials through LDS.
@@ -261,28 +261,30 @@ template <int FMT>
 __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u, std::uint32_t k, const XG& x0,
                                               const XG& x1, const IqLds* t) {
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    int ah[2] = {0, 0}, al[2] = {0, 0};
+    int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
       const uint2 gm = t->grid2[idx];
       const uint4 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
-      const std::uint32_t w0 = (gm.x ^ sm.x) + sm.z;
-      const std::uint32_t w1 = (gm.y ^ sm.y) + sm.w;
+      const int w0 = static_cast<int>((gm.x ^ sm.x) + sm.z);
+      const int w1 = static_cast<int>((gm.y ^ sm.y) + sm.w);
       const XG& xg = grp < 2 ? x0 : x1;
       const int o = (grp & 1) * 2, s = grp >> 1;
-      ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w0), static_cast<int>(xg.h[o]), ah[s], false);
-      ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w1), static_cast<int>(xg.h[o + 1]), ah[s], false);
-      al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w0), static_cast<int>(xg.l[o]), al[s], false);
-      al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w1), static_cast<int>(xg.l[o + 1]), al[s], false);
+      ah[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.h[o]), ah[s], false);
+      ah[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.h[o + 1]), ah[s], false);
+      am[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.m[o]), am[s], false);
+      am[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.m[o + 1]), am[s], false);
+      al[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.l[o]), al[s], false);
+      al[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.l[o + 1]), al[s], false);
     }
     const float d = h2f(r.c[0]);
     const float s0 = d * (0.5f + static_cast<float>(r.c[2] & 15u)) * 0.25f;
     const float s1 = d * (0.5f + static_cast<float>(r.c[2] >> 4)) * 0.25f;
-    return (s0 * x0.s) * static_cast<float>(ah[0] * 128 + al[0]) +
-           (s1 * x1.s) * static_cast<float>(ah[1] * 128 + al[1]);
+    return (s0 * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
+           (s1 * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    int ah[2] = {0, 0}, al[2] = {0, 0};
+    int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const uint4 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
@@ -293,15 +295,16 @@ __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u
         const int sel = 2 * grp + pair;
         const std::uint32_t qb = (r.a[sel >> 2] >> (8 * (sel & 3))) & 0xFFu;
         const std::uint32_t idx = qb | (((r.c[1] >> sel) & 1u) << 8);
-        const std::uint32_t w = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z);
-        ah[s] = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(xg.h[o + pair]), ah[s], false);
-        al[s] = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(xg.l[o + pair]), al[s], false);
+        const int w = static_cast<int>((t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z));
+        ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o + pair]), ah[s], false);
+        am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o + pair]), am[s], false);
+        al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o + pair]), al[s], false);
       }
     }
     const std::uint32_t nib = (k & 1u) ? (r.c[2] >> 4) : (r.c[2] & 15u);
     const float scale = h2f(r.c[0]) * static_cast<float>(1u + 2u * nib);
-    return (scale * x0.s) * static_cast<float>(ah[0] * 128 + al[0]) +
-           (scale * x1.s) * static_cast<float>(ah[1] * 128 + al[1]);
+    return (scale * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
+           (scale * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   } else {
     const std::uint32_t g = u.g;
     std::uint32_t lo[4], hi[4];
@@ -360,12 +363,15 @@ __device__ __forceinline__ void permlane16_swap(float& a, float& b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
-// acc[j] holds lane partials of row j (T in {4, 8}); afterwards every lane of
-// [r * 64/T, (r+1) * 64/T) holds the full sum of row r. permlane swaps handle
-// lane bits 5 and 4, DPP the bits within 16-lane rows: 8 VALU ops for T = 4.
+// acc[j] holds lane partials of row j (T in {4, 8, 16}); afterwards every lane
+// of [r * 64/T, (r+1) * 64/T) holds the full sum of row r. Each halving step
+// keeps one half of the live rows per lane group and adds the partner's
+// partial of that half: lane bit 5 via permlane32_swap, bit 4 via
+// permlane16_swap, bit 3 via DPP row_ror:8 and bit 2 via row_half_mirror;
+// the lanes left sharing a row are then summed with DPP (8 VALU ops at T = 4).
 template <int T>
 __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane) {
-  static_assert(T == 4 || T == 8, "tile of 4 or 8 rows");
+  static_assert(T == 4 || T == 8 || T == 16, "tile of 4, 8 or 16 rows");
 #pragma unroll
   for (int j = 0; j < T / 2; ++j) {
     float a = acc[j], b = acc[j + T / 2];
@@ -378,23 +384,34 @@ __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane
     permlane16_swap(a, b);
     acc[j] = a + b;
   }
-  float v = acc[0];
-  if constexpr (T == 8) {
-    // lane bit 3: keep row 0 or 1 of the pair, send the other across ror 8
-    const bool up = (lane & 8u) != 0u;
-    const float keep = up ? acc[1] : acc[0];
-    const float send = up ? acc[0] : acc[1];
-    v = keep + dpp<kDppRowRor8>(send);
-    v += dpp<kDppRowHalfMirror>(v);
-    v += dpp<kDppQuadXor2>(v);
-    v += dpp<kDppQuadXor1>(v);
-  } else {
+  if constexpr (T == 4) {
+    float v = acc[0];
     v += dpp<kDppRowRor8>(v);
     v += dpp<kDppRowRor4>(v);
     v += dpp<kDppRowRor2>(v);
     v += dpp<kDppRowRor1>(v);
+    return v;
+  } else {
+    const bool b3 = (lane & 8u) != 0u;
+#pragma unroll
+    for (int j = 0; j < T / 8; ++j) {
+      const float keep = b3 ? acc[j + T / 8] : acc[j];
+      const float send = b3 ? acc[j] : acc[j + T / 8];
+      acc[j] = keep + dpp<kDppRowRor8>(send);
+    }
+    float v = acc[0];
+    if constexpr (T == 16) {
+      const bool b2 = (lane & 4u) != 0u;
+      const float keep = b2 ? acc[1] : acc[0];
+      const float send = b2 ? acc[0] : acc[1];
+      v = keep + dpp<kDppRowHalfMirror>(send);
+    } else {
+      v += dpp<kDppRowHalfMirror>(v);
+    }
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppQuadXor1>(v);
+    return v;
   }
-  return v;
 }
 
 // ---- the kernel -------------------------------------------------------------
@@ -408,7 +425,10 @@ constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slot
 // the CUs, and loads the next tile's rows before it computes the current one.
 template <int FMT, int UPL, int TILE, bool SELF, class Epi>
 __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows, std::uint32_t ks,
-                                                  Epi epi) {
+                                                  Epi epi_arg) {
+  static_assert(Epi::kTile == TILE, "epilogue tile");
+  Epi epi = epi_arg;
+  epi.init(threadIdx.x & 63u);
   // Column-split partials, one slot per wave, double buffered by round parity
   // so a fast wave cannot overwrite a slot another wave still reads.
   __shared__ float part[2][kMaxKs][TILE];
@@ -514,7 +534,9 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
 // first lane of each range.
 template <int TILE>
 struct EpiStore {
+  static constexpr int kTile = TILE;
   float* y;
+  __device__ __forceinline__ void init(std::uint32_t) {}
   __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane,
                                              std::uint32_t rows) const {
     constexpr std::uint32_t spread = 64u / TILE;
@@ -528,10 +550,12 @@ struct EpiStore {
 // active_pages.
 template <int TILE>
 struct EpiDecode {
+  static constexpr int kTile = TILE;
   float* y;
   float* kv;
   const std::uint32_t* token;
   std::uint32_t kv_words, page_words, active_pages;
+  __device__ __forceinline__ void init(std::uint32_t) {}
   __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane,
                                              std::uint32_t rows) const {
     constexpr std::uint32_t spread = 64u / TILE;

@@ -1,0 +1,82 @@
+// Host-side launch of mv_kernel: geometry selection and the format switch,
+// shared by the matvec entry points and the layer pipeline's fused matvecs.
+#pragma once
+
+#include "mv.cuh"
+
+namespace rtxllm {
+
+inline int num_cus() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cached = n;
+    else
+      cached = 256;
+  }
+  return cached;
+}
+
+// Launch geometry of mv_kernel, from a sweep on MI355X at the 8B shapes: one
+// unit (32 columns) per lane for rows of up to 16384 columns (two beyond),
+// ks = ceil(units / 64) waves per row, nrg = 4 / ks row groups per workgroup
+// (at least 1), and one 4-row tile per row group: many small workgroups keep
+// enough loads in flight and the dispatcher's tail short.
+struct MvGeom {
+  int upl;
+  unsigned ks, nrg, grid;
+};
+
+inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, MvGeom& g) {
+  (void)fmt;
+  const std::uint32_t units = cols / 32u;
+  g.upl = units > 512u ? 2 : 1;
+  g.ks = (units + 64u * g.upl - 1u) / (64u * g.upl);
+  if (g.ks > static_cast<unsigned>(kMaxKs)) return false;
+  g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
+  const std::uint32_t tiles = (rows + tile - 1) / tile;
+  const std::uint32_t grid = (tiles + g.nrg - 1) / g.nrg;
+  g.grid = grid < 1u ? 1u : (grid > 1048576u ? 1048576u : grid);
+  return true;
+}
+
+template <int FMT, bool SELF, class Epi>
+inline hipError_t launch_mv_fmt(const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
+                         hipStream_t stream) {
+  constexpr int kT = Epi::kTile;
+  MvGeom g;
+  if (!mv_geom(FMT, row_count, w.cols, kT, g)) return hipErrorInvalidValue;
+  const dim3 grid(g.grid), block(64u * g.ks * g.nrg);
+  if (g.upl == 2) {
+    hipLaunchKernelGGL((mv_kernel<FMT, 2, kT, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
+  } else {
+    hipLaunchKernelGGL((mv_kernel<FMT, 1, kT, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
+  }
+  return hipGetLastError();
+}
+
+template <bool SELF, class Epi>
+inline hipError_t launch_mv(int fmt, const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
+                     hipStream_t stream) {
+  switch (fmt) {
+    case RTXLLM_FMT_Q4K_RAW: return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q4K_SPLIT_PREDECODED:
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_PREDECODED, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q4K_SPLIT_HALF:
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_HALF, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q4K_SPLIT_COMPACT:
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_COMPACT, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q5K: return launch_mv_fmt<RTXLLM_FMT_Q5K, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_IQ2S: return launch_mv_fmt<RTXLLM_FMT_IQ2S, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_IQ3S: return launch_mv_fmt<RTXLLM_FMT_IQ3S, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_Q4K_RAW_PREDECODED:
+      return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED, SELF>(w, xs, row_count, epi, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace rtxllm

@@ -36,6 +36,14 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_matvec": [c_int, _P, _P, _P, _P, _U, _U, _S],
     "rtxllm_stage_activation": [_P, _P, _U, _P, _S],
     "rtxllm_matvec_xq": [c_int, _P, _P, _P, _P, _U, _U, _S],
+    "rtxllm_llama_create": [_P, _P],
+    "rtxllm_llama_upload": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
+    "rtxllm_llama_download": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
+    "rtxllm_llama_synth_weights": [_P, c_uint64, _S],
+    "rtxllm_llama_forward": [_P, _U, _U, c_int, _S],
+    "rtxllm_llama_step": [_P, _S],
+    "rtxllm_llama_graph_capture": [_P, _S],
+    "rtxllm_llama_graph_replay": [_P, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",
@@ -61,6 +69,9 @@ _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_format_payload_block_bytes": (c_uint32, [c_int]),
     "rtxllm_format_meta_block_bytes": (c_uint32, [c_int]),
     "rtxllm_xq_bytes": (c_size_t, [c_uint32]),
+    "rtxllm_llama_destroy": (None, [_P]),
+    "rtxllm_llama_region": (_P, [_P, ctypes.c_char_p, _U, _P]),
+    "rtxllm_llama_launches_per_step": (c_uint32, [_P]),
     "rtxllm_q4k_split_pack": (c_int, [c_int, _P, c_size_t, _P, _P]),
     "rtxllm_synth_raw_blocks": (c_int, [c_int, c_uint64, c_size_t, c_float, c_float, _P, c_int]),
     "rtxllm_synth_normal_f32": (c_int, [c_uint64, c_size_t, c_float, c_float, _P, c_int]),

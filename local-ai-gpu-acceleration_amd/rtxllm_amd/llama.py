@@ -1,0 +1,140 @@
+"""Python handle on the C-ABI Llama decode runner (include/rtxllm/llama.h).
+
+The runner owns its VRAM arena; this wrapper only passes configuration,
+host arrays to upload, and the HIP stream. Every computation runs in
+build/librtxllm.so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_uint32, c_uint64, c_void_p, c_size_t
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import formats as F
+from ._lib import check, lib
+
+
+class LlamaConfig(ctypes.Structure):
+    _fields_ = [(n, c_uint32) for n in ("hidden", "n_heads", "n_kv_heads", "ffn", "vocab", "n_layers", "max_ctx",
+                                         "page_size")] + [
+        ("rope_theta", c_float),
+        ("rms_eps", c_float),
+    ] + [(n, c_int) for n in ("fmt_qkv", "fmt_o", "fmt_gate_up", "fmt_down", "fmt_lm_head")]
+
+
+EMBED, HEAD = 1, 2
+HEAD_DIM = 128
+
+# Formats of the 8B mixed-quant configuration: q/k/v/o IQ3_S, gate/up IQ2_S,
+# down Q4_K (resident split-native pack), embedding and LM head Q5_K.
+MIXED_8B_FORMATS = dict(fmt_qkv=F.IQ3S, fmt_o=F.IQ3S, fmt_gate_up=F.IQ2S, fmt_down=F.Q4K_SPLIT_NATIVE,
+                        fmt_lm_head=F.Q5K)
+
+
+@dataclass
+class Shape:
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    ffn: int
+    vocab: int
+    n_layers: int
+    max_ctx: int
+    page_size: int = 64
+    rope_theta: float = 500000.0
+    rms_eps: float = 1e-6
+
+    def config(self, formats: dict | None = None) -> LlamaConfig:
+        f = dict(MIXED_8B_FORMATS)
+        f.update(formats or {})
+        return LlamaConfig(self.hidden, self.n_heads, self.n_kv_heads, self.ffn, self.vocab, self.n_layers,
+                           self.max_ctx, self.page_size, self.rope_theta, self.rms_eps, f["fmt_qkv"], f["fmt_o"],
+                           f["fmt_gate_up"], f["fmt_down"], f["fmt_lm_head"])
+
+
+LLAMA_8B = Shape(hidden=4096, n_heads=32, n_kv_heads=8, ffn=14336, vocab=128256, n_layers=32, max_ctx=4096)
+
+
+def tensor_seed(seed: int, layer: int | None, role: str) -> int:
+    """Seed of one synthetic weight tensor (rtxllm_llama_synth_weights)."""
+    roles = {"qkv": 1, "o": 2, "gate_up": 3, "down": 4}
+    if role == "embed":
+        return seed + 5
+    if role == "lm_head":
+        return seed + 6
+    return seed + 4096 * (layer + 1) + roles[role]
+
+
+class Llama:
+    def __init__(self, shape: Shape, formats: dict | None = None):
+        self.shape = shape
+        self.cfg = shape.config(formats)
+        self.formats = {k: getattr(self.cfg, k) for k in MIXED_8B_FORMATS}
+        handle = c_void_p()
+        check("rtxllm_llama_create", lib().rtxllm_llama_create(ctypes.byref(self.cfg), ctypes.byref(handle)))
+        self.h = handle.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().rtxllm_llama_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- regions -------------------------------------------------------------
+    def region_bytes(self, name: str, layer: int = 0) -> int:
+        n = c_size_t()
+        p = lib().rtxllm_llama_region(self.h, name.encode(), layer, ctypes.byref(n))
+        if not p:
+            raise KeyError(name)
+        return n.value
+
+    def region_ptr(self, name: str, layer: int = 0) -> int:
+        p = lib().rtxllm_llama_region(self.h, name.encode(), layer, None)
+        if not p:
+            raise KeyError(name)
+        return p
+
+    def upload(self, name: str, arr: np.ndarray, layer: int = 0, offset: int = 0) -> None:
+        a = np.ascontiguousarray(arr)
+        check("rtxllm_llama_upload", lib().rtxllm_llama_upload(self.h, name.encode(), layer, offset,
+                                                                a.ctypes.data_as(c_void_p), a.nbytes))
+
+    def download(self, name: str, dtype, count: int | None = None, layer: int = 0, offset: int = 0) -> np.ndarray:
+        itemsize = np.dtype(dtype).itemsize
+        if count is None:
+            count = (self.region_bytes(name, layer) - offset) // itemsize
+        out = np.empty(count, dtype=dtype)
+        check("rtxllm_llama_download", lib().rtxllm_llama_download(self.h, name.encode(), layer, offset,
+                                                                    out.ctypes.data_as(c_void_p), out.nbytes))
+        return out
+
+    # -- execution --------------------------------------------------------------
+    def synth_weights(self, seed: int, stream: int = 0) -> None:
+        check("rtxllm_llama_synth_weights", lib().rtxllm_llama_synth_weights(self.h, seed, stream))
+
+    def forward(self, first: int, last: int, flags: int, stream: int = 0) -> None:
+        check("rtxllm_llama_forward", lib().rtxllm_llama_forward(self.h, first, last, flags, stream))
+
+    def step(self, stream: int = 0) -> None:
+        check("rtxllm_llama_step", lib().rtxllm_llama_step(self.h, stream))
+
+    def graph_capture(self, stream: int) -> None:
+        check("rtxllm_llama_graph_capture", lib().rtxllm_llama_graph_capture(self.h, stream))
+
+    def graph_replay(self, stream: int) -> None:
+        check("rtxllm_llama_graph_replay", lib().rtxllm_llama_graph_replay(self.h, stream))
+
+    def launches_per_step(self) -> int:
+        return int(lib().rtxllm_llama_launches_per_step(self.h))
+
+    def set_token_pos(self, token: int, pos: int) -> None:
+        self.upload("token", np.array([token], np.uint32))
+        self.upload("pos", np.array([pos], np.uint32))

@@ -341,25 +341,29 @@ void orc_q4k_split(int fmt, const uint8_t* raw, size_t n_blocks, uint8_t* payloa
   }
 }
 
-void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* l,
+void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* m, int8_t* l,
                           float* scale, float* sum) {
+  const float K = 2080768.0f; /* 127 * 16384 */
   for (uint32_t g = 0; g < cols / 16u; ++g) {
     float v[16];
-    float m = 0.0f;
+    float mx = 0.0f;
     for (int j = 0; j < 16; ++j) {
       v[j] = weight ? x[16u * g + j] * weight[16u * g + j] : x[16u * g + j];
       const float a = fabsf(v[j]);
-      if (a > m) m = a; /* NaN never compares greater: ignored, as fmaxf does */
+      if (a > mx) mx = a; /* NaN never compares greater: ignored, as fmaxf does */
     }
-    const float inv = m > 0.0f ? 16256.0f / m : 0.0f;
-    scale[g] = m / 16256.0f;
+    const float inv = mx > 0.0f ? K / mx : 0.0f;
+    scale[g] = mx / K;
     int total = 0;
     for (int j = 0; j < 16; ++j) {
       const float r = rintf(v[j] * inv);
-      int X = isnan(r) ? 0 : (r > 16256.0f ? 16256 : (r < -16256.0f ? -16256 : (int)r));
-      const int H = (int)floor((X + 64) / 128.0);
+      const int X = isnan(r) ? 0 : (r > K ? 2080768 : (r < -K ? -2080768 : (int)r));
+      const int H = (int)floor((X + 8192) / 16384.0);
+      const int R = X - 16384 * H;
+      const int M = (int)floor((R + 64) / 128.0);
       h[16u * g + j] = (int8_t)H;
-      l[16u * g + j] = (int8_t)(X - 128 * H);
+      m[16u * g + j] = (int8_t)M;
+      l[16u * g + j] = (int8_t)(R - 128 * M);
       total += X;
     }
     sum[g] = scale[g] * (float)total;
@@ -369,7 +373,7 @@ void orc_stage_activation(const float* x, const float* weight, uint32_t cols, in
 typedef struct {
   int fmt;
   const uint8_t *payload, *meta;
-  const int8_t *h, *l;
+  const int8_t *h, *m, *l;
   const float* scale;
   uint32_t cols, r0, r1;
   double* y;
@@ -384,11 +388,11 @@ static void* st_worker(void* arg) {
     for (uint32_t b = 0; b < bpr; ++b) {
       const size_t bi = (size_t)r * bpr + b;
       const uint8_t* p = blk_ptr(j->payload, pb, bi);
-      const uint8_t* m = blk_ptr(j->meta, mb, bi);
+      const uint8_t* mt = blk_ptr(j->meta, mb, bi);
       for (uint32_t v = 0; v < 256u; ++v) {
         const uint32_t c = b * 256u + v;
-        const double xh = (double)j->scale[c / 16u] * (128.0 * j->h[c] + j->l[c]);
-        acc += (double)orc_dequant_value(j->fmt, p, m, v) * xh;
+        const double X = 16384.0 * j->h[c] + 128.0 * j->m[c] + j->l[c];
+        acc += (double)orc_dequant_value(j->fmt, p, mt, v) * ((double)j->scale[c / 16u] * X);
       }
     }
     j->y[r] = acc;
@@ -396,15 +400,16 @@ static void* st_worker(void* arg) {
   return NULL;
 }
 
-void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* l,
-                           const float* scale, uint32_t rows, uint32_t cols, double* y, int nthreads) {
+void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* m,
+                           const int8_t* l, const float* scale, uint32_t rows, uint32_t cols, double* y,
+                           int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > 64) nthreads = 64;
   if ((uint32_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
   st_job jobs[64];
   pthread_t th[64];
   for (int t = 0; t < nthreads; ++t) {
-    st_job jb = {fmt, payload, meta, h, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
+    st_job jb = {fmt, payload, meta, h, m, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
                  (uint32_t)((uint64_t)rows * (t + 1) / nthreads), y};
     jobs[t] = jb;
   }

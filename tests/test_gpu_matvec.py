@@ -227,3 +227,6 @@ def test_matvec_xq_equals_self_staging_and_staged_oracle(orc, fmt, shape):
     ref = orc.matvec_staged_f64(of, pl, mt, x, rows, cols, 8)
     # same staged digits: only fp32 rounding of the per-group products separates them
     assert np.max(np.abs(y_xq - ref)) / np.max(np.abs(ref)) < 1e-5
+    # and the staged product is an fp32-grade matvec: close to the float64 oracle on the raw x
+    ref64 = orc.matvec_f64(of, pl, mt, x, rows, cols, 8)
+    assert np.max(np.abs(y_xq - ref64)) / np.max(np.abs(ref64)) < 2e-5
