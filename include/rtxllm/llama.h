@@ -81,6 +81,11 @@ hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream);
 /* Capture one decode step into the model's hipGraph / replay it. */
 hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream);
 hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream);
+/* One stage of the step alone, on the current state, for per-stage timing (the
+ * reference runner's per-phase replay timing, main.cpp:4838-4869): stage 0
+ * embedding gather + staging, 1 qkv of `layer`, 2 attention of `layer`, 3 o,
+ * 4 gate/up, 5 down, 6 LM head + argmax. */
+hipError_t rtxllm_llama_launch_stage(rtxllm_llama* m, uint32_t layer, int stage, hipStream_t stream);
 /* Kernel launches per decode step. */
 uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m);
 

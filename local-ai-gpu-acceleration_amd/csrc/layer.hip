@@ -144,7 +144,9 @@ struct EpiLogits {
     key = other > key ? other : key;
     other = __shfl_xor(key, 32, 64);
     key = other > key ? other : key;
-    if (lane == 0u && key != 0ull) atomicMax(argkey, key);
+    // Most tiles lose to the running maximum: read it first (a plain L2 read)
+    // and only then contend for the atomic.
+    if (lane == 0u && key != 0ull && key > __builtin_nontemporal_load(argkey)) atomicMax(argkey, key);
   }
 };
 
@@ -235,133 +237,153 @@ __global__ __launch_bounds__(1024) void embed_q5k_kernel(const std::uint8_t* __r
 
 // ---- attention -------------------------------------------------------------------
 
-constexpr std::uint32_t kAttnThreads = 256;
+constexpr std::uint32_t kAttnChunk = 64;  // positions per workgroup (one wave)
 constexpr std::uint32_t kMaxGroup = 8;
 
-__host__ __device__ inline std::uint32_t attn_chunk(std::uint32_t max_ctx, std::uint32_t n_kv) {
-  std::uint32_t want = max_ctx * n_kv / 256u, p = 32u;
-  while (p * 2u <= want && p < 256u) p *= 2u;
-  return p;
-}
-
-// Workgroup (chunk c, kv head g): the `group` query heads of g over positions
-// [c P, (c + 1) P) ∩ [0, pos]: scores (thread = position), chunk softmax
-// (max m, sum l of exp(s - m)) and o = sum_t exp(s_t - m) v_t (thread = dim).
+// One wave per (chunk c of 64 positions, kv head g): the `GROUP` query heads of
+// g over positions [64 c, 64 c + 64) ∩ [0, pos].
+//  * scores: lane = position; the lane streams its K row (256 B) and dots it
+//    with the heads' q, which every lane reads at the same address (scalar
+//    loads, broadcast);
+//  * chunk softmax per head: m = max, p = exp(s - m), l = sum p (wave
+//    reductions);
+//  * o = sum_p p_p v_p: lane = dimension pair, the wave walks the positions,
+//    taking p_p by readlane and the V row as one coalesced 256 B load.
 // Partial record per head: m, l, o[128].
-__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
-                                                                    std::uint32_t group, const std::uint32_t* pos_ptr,
-                                                                    std::uint32_t chunk, std::uint32_t nchunks,
-                                                                    float* __restrict__ partials) {
-  __shared__ float qs[kMaxGroup][kHeadDim];
-  __shared__ float sc[kMaxGroup][256];
-  __shared__ float red[kMaxGroup][kAttnThreads / 64];
-  __shared__ float mrow[kMaxGroup], lrow[kMaxGroup];
-  const std::uint32_t c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
+template <int GROUP>
+__global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
+                                                          const std::uint32_t* __restrict__ pos_ptr,
+                                                          std::uint32_t nchunks, float* __restrict__ partials) {
+  const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x;
   const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
-  const std::uint32_t p0 = c * chunk;
-  float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * group * (kHeadDim + 2u);
+  const std::uint32_t p0 = c * kAttnChunk;
+  float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * GROUP * (kHeadDim + 2u);
   if (p0 > pos) {  // chunk beyond the context: empty record
-    for (std::uint32_t i = t; i < group * (kHeadDim + 2u); i += blockDim.x) {
-      const std::uint32_t f = i % (kHeadDim + 2u);
-      rec[i] = f == 0u ? -INFINITY : 0.0f;
-    }
+    for (std::uint32_t i = lane; i < GROUP * (kHeadDim + 2u); i += 64u)
+      rec[i] = (i % (kHeadDim + 2u)) == 0u ? -INFINITY : 0.0f;
     return;
   }
+  const std::uint32_t npos = (pos - p0 + 1u) < kAttnChunk ? (pos - p0 + 1u) : kAttnChunk;
+  const bool valid = lane < npos;
+  const float* qg = q + static_cast<std::size_t>(g) * GROUP * kHeadDim;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
-  for (std::uint32_t i = t; i < group * kHeadDim; i += blockDim.x)
-    qs[i / kHeadDim][i % kHeadDim] = q[(g * group) * kHeadDim + i];
-  __syncthreads();
-  const std::uint32_t npos = (pos - p0 + 1u) < chunk ? (pos - p0 + 1u) : chunk;
-  for (std::uint32_t i = t; i < chunk; i += blockDim.x) {
-    float s[kMaxGroup];
-    for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] = -INFINITY;
-    if (i < npos) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kv.k + kv_offset(kv, p0 + i, g));
-      for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] = 0.0f;
-#pragma unroll 4
-      for (int w = 0; w < 16; ++w) {
-        const uint4 pk = kr[w];
-        const std::uint32_t words[4] = {pk.x, pk.y, pk.z, pk.w};
+
+  // This lane's position (clamped into the chunk's valid range, so every
+  // address is inside the cache) and its K / V row offset.
+  const std::size_t row_off = kv_offset(kv, p0 + (valid ? lane : 0u), g);
+  float s[GROUP];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
-          const int d = 8 * w + 2 * e;
-          for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] += qs[hh][d] * k0 + qs[hh][d + 1] * k1;
-        }
+  for (int h = 0; h < GROUP; ++h) s[h] = 0.0f;
+  {
+    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off);
+    uint4 pk[16];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) pk[w] = kr[w];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const std::uint32_t words[4] = {pk[w].x, pk[w].y, pk[w].z, pk[w].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
+        const int d = 8 * w + 2 * e;
+#pragma unroll
+        for (int h = 0; h < GROUP; ++h) s[h] += qg[h * kHeadDim + d] * k0 + qg[h * kHeadDim + d + 1] * k1;
       }
-      for (std::uint32_t hh = 0; hh < group; ++hh) s[hh] *= scale;
     }
-    for (std::uint32_t hh = 0; hh < group; ++hh) sc[hh][i] = s[hh];
   }
-  __syncthreads();
-  // chunk max and exp-sum per head
-  const std::uint32_t wave = t >> 6, lane = t & 63u, nw = blockDim.x >> 6;
-  for (std::uint32_t hh = 0; hh < group; ++hh) {
-    float m = -INFINITY;
-    for (std::uint32_t i = t; i < chunk; i += blockDim.x) m = fmaxf(m, sc[hh][i]);
-    m = wave_max(m);
-    if (lane == 0u) red[hh][wave] = m;
+  float pw[GROUP], mh[GROUP], lh[GROUP];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) {
+    const float sc = valid ? s[h] * scale : -INFINITY;
+    mh[h] = wave_max(sc);
+    pw[h] = valid ? expf(sc - mh[h]) : 0.0f;  // 0 for positions beyond the context
+    lh[h] = wave_sum(pw[h]);
   }
-  __syncthreads();
-  if (t < group) {
-    float m = red[t][0];
-    for (std::uint32_t i = 1; i < nw; ++i) m = fmaxf(m, red[t][i]);
-    mrow[t] = m;
-  }
-  __syncthreads();
-  for (std::uint32_t hh = 0; hh < group; ++hh) {
-    float l = 0.0f;
-    for (std::uint32_t i = t; i < chunk; i += blockDim.x) {
-      const float p = i < npos ? expf(sc[hh][i] - mrow[hh]) : 0.0f;
-      sc[hh][i] = p;
-      l += p;
+  // o = sum_i p_i v_i over the chunk's 64 positions (weights of invalid ones are
+  // 0 and their rows clamped in range); V rows fetched 16 at a time.
+  const int off_lo = static_cast<int>(row_off & 0xFFFFFFFFu), off_hi = static_cast<int>(row_off >> 32);
+  float o0[GROUP], o1[GROUP];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
+#pragma unroll
+  for (int i0 = 0; i0 < static_cast<int>(kAttnChunk); i0 += 16) {
+    std::uint32_t vw[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const std::size_t off = (static_cast<std::size_t>(static_cast<std::uint32_t>(
+                                   __builtin_amdgcn_readlane(off_hi, i0 + j))) << 32) |
+                              static_cast<std::uint32_t>(__builtin_amdgcn_readlane(off_lo, i0 + j));
+      vw[j] = *reinterpret_cast<const std::uint32_t*>(kv.v + off + 2u * lane);
     }
-    l = wave_sum(l);
-    if (lane == 0u) red[hh][wave] = l;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float v0 = h2f(vw[j]), v1 = h2f(vw[j] >> 16);
+#pragma unroll
+      for (int h = 0; h < GROUP; ++h) {
+        const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), i0 + j));
+        o0[h] += p * v0;
+        o1[h] += p * v1;
+      }
+    }
   }
-  __syncthreads();
-  if (t < group) {
-    float l = 0.0f;
-    for (std::uint32_t i = 0; i < nw; ++i) l += red[t][i];
-    lrow[t] = l;
-  }
-  __syncthreads();
-  // o[hh][d] = sum_i p[hh][i] v[i][d]
-  for (std::uint32_t o = t; o < group * kHeadDim; o += blockDim.x) {
-    const std::uint32_t hh = o / kHeadDim, d = o % kHeadDim;
-    float acc = 0.0f;
-    for (std::uint32_t i = 0; i < npos; ++i) acc += sc[hh][i] * h2f(kv.v[kv_offset(kv, p0 + i, g) + d]);
-    rec[hh * (kHeadDim + 2u) + 2u + d] = acc;
-  }
-  if (t < group) {
-    rec[t * (kHeadDim + 2u)] = mrow[t];
-    rec[t * (kHeadDim + 2u) + 1u] = lrow[t];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) {
+    float* r = rec + h * (kHeadDim + 2u);
+    *reinterpret_cast<float2*>(r + 2u + 2u * lane) = make_float2(o0[h], o1[h]);
+    if (lane == 0u) {
+      r[0] = mh[h];
+      r[1] = lh[h];
+    }
   }
 }
 
-// One workgroup per query head, thread = dim: merge the chunk records
-// (m_c, l_c, o_c) of its kv head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c.
-__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __restrict__ partials,
-                                                                std::uint32_t group, const std::uint32_t* pos_ptr,
-                                                                std::uint32_t capacity, std::uint32_t chunk,
-                                                                std::uint32_t nchunks, float* __restrict__ att) {
-  const std::uint32_t head = blockIdx.x, d = threadIdx.x;
+// One wave per query head: merge the chunk records (m_c, l_c, o_c) of its kv
+// head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c. Per pass of 64
+// chunks, lane c reads chunk c's (m, l) (wave max / sum), then lane = dimension
+// pair accumulates the weighted o_c, the weights taken by readlane; running
+// sums are rescaled when a later pass raises the maximum.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
+                                                          const std::uint32_t* pos_ptr, std::uint32_t capacity,
+                                                          std::uint32_t nchunks, float* __restrict__ att) {
+  const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
   const std::uint32_t g = head / group, hh = head % group;
   const std::uint32_t pos = *pos_ptr < capacity ? *pos_ptr : capacity - 1u;
-  const std::uint32_t active = pos / chunk + 1u;
+  const std::uint32_t active = pos / kAttnChunk + 1u;
   const std::uint32_t n = active < nchunks ? active : nchunks;
-  const float* base = partials + (static_cast<std::size_t>(g) * nchunks) * group * (kHeadDim + 2u) +
-                      hh * (kHeadDim + 2u);
-  const std::size_t stride = group * (kHeadDim + 2u);
-  float M = -INFINITY;
-  for (std::uint32_t c = 0; c < n; ++c) M = fmaxf(M, base[c * stride]);
-  float L = 0.0f, o = 0.0f;
-  for (std::uint32_t c = 0; c < n; ++c) {
-    const float w = expf(base[c * stride] - M);
-    L += w * base[c * stride + 1u];
-    o += w * base[c * stride + 2u + d];
+  const std::size_t stride = static_cast<std::size_t>(group) * (kHeadDim + 2u);
+  const float* base = partials + static_cast<std::size_t>(g) * nchunks * stride + hh * (kHeadDim + 2u);
+  float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (std::uint32_t c0 = 0; c0 < n; c0 += 64u) {
+    const std::uint32_t c = c0 + lane;
+    const bool ok = c < n;
+    const float m = ok ? base[c * stride] : -INFINITY;
+    const float l = ok ? base[c * stride + 1u] : 0.0f;
+    const float Mn = fmaxf(M, wave_max(m));  // finite: chunk 0 always holds position 0
+    const float r = expf(M - Mn);            // 0 on the first pass
+    L *= r, o0 *= r, o1 *= r;
+    const float w = ok ? expf(m - Mn) : 0.0f;
+    L += wave_sum(w * l);
+    M = Mn;
+    const std::uint32_t cnt = n - c0 < 64u ? n - c0 : 64u;
+    for (std::uint32_t j0 = 0; j0 < cnt; j0 += 8u) {
+      float2 ov[8];
+#pragma unroll
+      for (std::uint32_t j = 0; j < 8u; ++j) {
+        const std::uint32_t cj = c0 + (j0 + j < cnt ? j0 + j : cnt - 1u);
+        ov[j] = *reinterpret_cast<const float2*>(base + cj * stride + 2u + 2u * lane);
+      }
+#pragma unroll
+      for (std::uint32_t j = 0; j < 8u; ++j) {
+        const float wj = j0 + j < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                      __builtin_bit_cast(int, w),
+                                                                      static_cast<int>(j0 + j)))
+                                      : 0.0f;
+        o0 += wj * ov[j].x;
+        o1 += wj * ov[j].y;
+      }
+    }
   }
-  att[head * kHeadDim + d] = o / L;
+  *reinterpret_cast<float2*>(att + head * kHeadDim + 2u * lane) = make_float2(o0 / L, o1 / L);
 }
 
 __global__ void argmax_finalize_kernel(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
@@ -416,8 +438,7 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
 }
 
 std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx) {
-  const std::uint32_t chunk = attn_chunk(max_ctx, n_kv);
-  const std::uint32_t nchunks = (max_ctx + chunk - 1u) / chunk;
+  const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
   return static_cast<std::size_t>(n_kv) * nchunks * (n_heads / n_kv) * (kHeadDim + 2u);
 }
 
@@ -427,14 +448,19 @@ hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_h
       kv.capacity > max_ctx)
     return hipErrorInvalidValue;
   const std::uint32_t group = n_heads / kv.n_kv;
-  const std::uint32_t chunk = attn_chunk(max_ctx, kv.n_kv);
-  const std::uint32_t nchunks = (max_ctx + chunk - 1u) / chunk;
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(nchunks, kv.n_kv), dim3(kAttnThreads), 0, stream, q, kv, group, pos,
-                     chunk, nchunks, partials);
+  const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
+  const dim3 grid(nchunks, kv.n_kv), block(64);
+  switch (group) {
+    case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
+    case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
+    case 4: hipLaunchKernelGGL(attn_partial_kernel<4>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
+    case 8: hipLaunchKernelGGL(attn_partial_kernel<8>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
+    default: return hipErrorInvalidValue;
+  }
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(kHeadDim), 0, stream, partials, group, pos,
-                     kv.capacity, chunk, nchunks, att);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, partials, group, pos, kv.capacity,
+                     nchunks, att);
   return hipGetLastError();
 }
 

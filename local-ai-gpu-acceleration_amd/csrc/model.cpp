@@ -220,51 +220,82 @@ extern "C" hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed,
   return st;
 }
 
-extern "C" hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint32_t last, int flags,
-                                           hipStream_t stream) {
-  if (m == nullptr || first > last || last > m->cfg.n_layers) return hipErrorInvalidValue;
+namespace {
+
+enum Stage { kEmbed = 0, kQkv = 1, kAttention = 2, kO = 3, kGateUp = 4, kDown = 5, kHead = 6 };
+
+// One stage of layer l; next_norm is the norm weight the down stage stages the
+// residual with (the next layer's attn_norm, or out_norm after the last layer).
+hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed, const float* next_norm,
+                        hipStream_t stream) {
   const rtxllm_llama_config& c = m->cfg;
   auto* h = region<float>(m, "h");
   void* xq = m->arena.arena_ptr("xq");
   auto* sumsq = region<float>(m, "sumsq");
-  auto* token = region<std::uint32_t>(m, "token");
   auto* pos = region<std::uint32_t>(m, "pos");
-  const float* first_norm = first < last ? region<float>(m, layer_name("attn_norm", first)) : region<float>(m, "out_norm");
-
-  hipError_t st = rtxllm::launch_embed_q5k((flags & RTXLLM_LLAMA_EMBED) ? region<std::uint8_t>(m, "embed") : nullptr,
-                                           c.hidden, c.vocab, token, h, first_norm, xq, sumsq, m->nslots, stream);
   const rtxllm::NormIn in{xq, sumsq, m->nslots, c.hidden, c.rms_eps};
+  switch (stage) {
+    case kEmbed:
+      return rtxllm::launch_embed_q5k(embed ? region<std::uint8_t>(m, "embed") : nullptr, c.hidden, c.vocab,
+                                      region<std::uint32_t>(m, "token"), h, next_norm, xq, sumsq, m->nslots, stream);
+    case kQkv: {
+      const TensorRef t = tensor(m, layer_name("qkv", l));
+      return rtxllm::launch_qkv(c.fmt_qkv, t.payload, t.meta, c.hidden, in, m->q_rows, m->kv_rows,
+                                region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv_layer(m, l), stream);
+    }
+    case kAttention:
+      return rtxllm::launch_attention(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
+                                      region<float>(m, "attn_partials"), region<float>(m, "att"), stream);
+    case kO: {
+      const TensorRef t = tensor(m, layer_name("o", l));
+      return rtxllm::launch_residual(c.fmt_o, t.payload, t.meta, c.hidden, m->q_rows, region<float>(m, "att"), h,
+                                     region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
+    }
+    case kGateUp: {
+      const TensorRef t = tensor(m, layer_name("gate_up", l));
+      return rtxllm::launch_gate_up(c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn, c.hidden, in,
+                                    region<float>(m, "act"), stream);
+    }
+    case kDown: {
+      const TensorRef t = tensor(m, layer_name("down", l));
+      return rtxllm::launch_residual(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, region<float>(m, "act"), h,
+                                     next_norm, xq, sumsq, stream);
+    }
+    case kHead: {
+      const TensorRef t = tensor(m, "lm_head");
+      auto* argkey = region<unsigned long long>(m, "argkey");
+      const hipError_t st = rtxllm::launch_logits(c.fmt_lm_head, t.payload, t.meta, c.vocab, c.hidden, in,
+                                                  region<float>(m, "logits"), argkey, stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_argmax_finalize(argkey, region<std::uint32_t>(m, "token"), pos, 1u, stream);
+    }
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint32_t last, int flags,
+                                           hipStream_t stream) {
+  if (m == nullptr || first > last || last > m->cfg.n_layers) return hipErrorInvalidValue;
+  const float* out_norm = region<float>(m, "out_norm");
+  const float* first_norm = first < last ? region<float>(m, layer_name("attn_norm", first)) : out_norm;
+  hipError_t st = launch_stage(m, 0u, kEmbed, (flags & RTXLLM_LLAMA_EMBED) != 0, first_norm, stream);
   for (std::uint32_t l = first; l < last && st == hipSuccess; ++l) {
-    const rtxllm::KvLayer kv = kv_layer(m, l);
-    const TensorRef qkv = tensor(m, layer_name("qkv", l));
-    st = rtxllm::launch_qkv(c.fmt_qkv, qkv.payload, qkv.meta, c.hidden, in, m->q_rows, m->kv_rows,
-                            region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv, stream);
-    if (st != hipSuccess) break;
-    st = rtxllm::launch_attention(region<float>(m, "q"), kv, c.n_heads, pos, c.max_ctx,
-                                  region<float>(m, "attn_partials"), region<float>(m, "att"), stream);
-    if (st != hipSuccess) break;
-    const TensorRef o = tensor(m, layer_name("o", l));
-    st = rtxllm::launch_residual(c.fmt_o, o.payload, o.meta, c.hidden, m->q_rows, region<float>(m, "att"), h,
-                                 region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
-    if (st != hipSuccess) break;
-    const TensorRef gu = tensor(m, layer_name("gate_up", l));
-    st = rtxllm::launch_gate_up(c.fmt_gate_up, gu.payload, gu.meta, 2u * c.ffn, c.hidden, in, region<float>(m, "act"),
-                                stream);
-    if (st != hipSuccess) break;
-    const TensorRef dn = tensor(m, layer_name("down", l));
-    const float* next_norm =
-        l + 1u < last ? region<float>(m, layer_name("attn_norm", l + 1u)) : region<float>(m, "out_norm");
-    st = rtxllm::launch_residual(c.fmt_down, dn.payload, dn.meta, c.hidden, c.ffn, region<float>(m, "act"), h,
-                                 next_norm, xq, sumsq, stream);
+    const float* next_norm = l + 1u < last ? region<float>(m, layer_name("attn_norm", l + 1u)) : out_norm;
+    for (int stage = kQkv; stage <= kDown && st == hipSuccess; ++stage)
+      st = launch_stage(m, l, stage, false, next_norm, stream);
   }
-  if (st == hipSuccess && (flags & RTXLLM_LLAMA_HEAD)) {
-    const TensorRef lm = tensor(m, "lm_head");
-    auto* argkey = region<unsigned long long>(m, "argkey");
-    st = rtxllm::launch_logits(c.fmt_lm_head, lm.payload, lm.meta, c.vocab, c.hidden, in, region<float>(m, "logits"),
-                               argkey, stream);
-    if (st == hipSuccess) st = rtxllm::launch_argmax_finalize(argkey, token, pos, 1u, stream);
-  }
+  if (st == hipSuccess && (flags & RTXLLM_LLAMA_HEAD)) st = launch_stage(m, 0u, kHead, false, out_norm, stream);
   return st;
+}
+
+extern "C" hipError_t rtxllm_llama_launch_stage(rtxllm_llama* m, uint32_t layer, int stage, hipStream_t stream) {
+  if (m == nullptr || layer >= m->cfg.n_layers || stage < kEmbed || stage > kHead) return hipErrorInvalidValue;
+  const float* next_norm = layer + 1u < m->cfg.n_layers ? region<float>(m, layer_name("attn_norm", layer + 1u))
+                                                        : region<float>(m, "out_norm");
+  if (stage == kEmbed) next_norm = region<float>(m, layer_name("attn_norm", 0u));
+  return launch_stage(m, layer, stage, stage == kEmbed, next_norm, stream);
 }
 
 extern "C" hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream) {

@@ -44,6 +44,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_step": [_P, _S],
     "rtxllm_llama_graph_capture": [_P, _S],
     "rtxllm_llama_graph_replay": [_P, _S],
+    "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",

@@ -132,6 +132,11 @@ class Llama:
     def graph_replay(self, stream: int) -> None:
         check("rtxllm_llama_graph_replay", lib().rtxllm_llama_graph_replay(self.h, stream))
 
+    STAGES = {"embed": 0, "qkv": 1, "attention": 2, "o": 3, "gate_up": 4, "down": 5, "lm_head": 6}
+
+    def launch_stage(self, layer: int, stage: str, stream: int = 0) -> None:
+        check("rtxllm_llama_launch_stage", lib().rtxllm_llama_launch_stage(self.h, layer, self.STAGES[stage], stream))
+
     def launches_per_step(self) -> int:
         return int(lib().rtxllm_llama_launches_per_step(self.h))
 
