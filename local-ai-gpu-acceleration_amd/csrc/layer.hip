@@ -37,8 +37,20 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 // all consumers see the same value.
 __device__ __forceinline__ float inv_rms(const float* __restrict__ sumsq, std::uint32_t nslots, std::uint32_t n,
                                          float eps, std::uint32_t lane) {
+  // lane adds sumsq[lane], sumsq[lane + 64], ... in that order; the loads of
+  // four steps are issued together
   float s = 0.0f;
-  for (std::uint32_t i = lane; i < nslots; i += 64u) s += sumsq[i];
+  for (std::uint32_t i0 = lane; i0 < nslots; i0 += 256u) {
+    float v[4];
+#pragma unroll
+    for (std::uint32_t j = 0; j < 4u; ++j) {
+      const std::uint32_t i = i0 + 64u * j;
+      const float t = sumsq[i < nslots ? i : nslots - 1u];
+      v[j] = i < nslots ? t : 0.0f;
+    }
+#pragma unroll
+    for (std::uint32_t j = 0; j < 4u; ++j) s += v[j];
+  }
   s = wave_sum(s);
   return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
 }
@@ -150,22 +162,25 @@ struct EpiLogits {
   }
 };
 
-// TILE 16: row r of the tile in lanes [4 r, 4 r + 4).
+// Residual add and next-norm staging over 16-row groups (one staged group of
+// the next matvec's input): lane i < 16 of wave 0 owns row row0 + i.
 struct EpiResidual {
-  static constexpr int kTile = 16;
+  static constexpr int kTile = 4;
+  static constexpr std::uint32_t kGroupRows = kXGroup;
   float* h;
   const float* w_next;
   XQOut xq;
   float* sumsq;
   __device__ __forceinline__ void init(std::uint32_t) {}
-  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t) const {
-    const std::uint32_t row = row0 + (lane >> 2);
-    const bool owner = (lane & 3u) == 0u;
-    const float hn = h[row] + v;
+  __device__ __forceinline__ void group(std::uint32_t row0, const float* vals, std::uint32_t lane,
+                                        std::uint32_t) const {
+    const bool owner = lane < kXGroup;
+    const std::uint32_t row = row0 + (owner ? lane : 0u);
+    const float hn = h[row] + (owner ? vals[lane] : 0.0f);
     if (owner) h[row] = hn;
     const float sq = wave_sum(owner ? hn * hn : 0.0f);
     // stage the 16-value group h * w_next exactly as quant16 does
-    const float x = w_next != nullptr ? hn * w_next[row] : hn;
+    const float x = owner ? (w_next != nullptr ? hn * w_next[row] : hn) : 0.0f;
     const float m = wave_max(fabsf(x));
     const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
     const float s = m / kXQLimitF;
@@ -241,14 +256,14 @@ constexpr std::uint32_t kAttnChunk = 64;  // positions per workgroup (one wave)
 constexpr std::uint32_t kMaxGroup = 8;
 
 // One wave per (chunk c of 64 positions, kv head g): the `GROUP` query heads of
-// g over positions [64 c, 64 c + 64) ∩ [0, pos].
-//  * scores: lane = position; the lane streams its K row (256 B) and dots it
-//    with the heads' q, which every lane reads at the same address (scalar
-//    loads, broadcast);
+// g over positions [64 c, 64 c + 64) ∩ [0, pos]. Every K and V load of the chunk
+// is issued up front (32 KB per wave in flight), then:
+//  * scores: lane = position; the lane dots its K row (256 B) with the heads'
+//    q, which every lane reads at the same address (scalar loads, broadcast);
 //  * chunk softmax per head: m = max, p = exp(s - m), l = sum p (wave
 //    reductions);
-//  * o = sum_p p_p v_p: lane = dimension pair, the wave walks the positions,
-//    taking p_p by readlane and the V row as one coalesced 256 B load.
+//  * o = sum_p p_p v_p: lane = dimension pair, V rows coalesced (256 B per
+//    position), p_p taken by readlane.
 // Partial record per head: m, l, o[128].
 template <int GROUP>
 __global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
@@ -269,26 +284,34 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restric
   const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
 
   // This lane's position (clamped into the chunk's valid range, so every
-  // address is inside the cache) and its K / V row offset.
-  const std::size_t row_off = kv_offset(kv, p0 + (valid ? lane : 0u), g);
+  // address is inside the cache) and its K / V row offset (elements; the host
+  // checks that a layer's cache has fewer than 2^32 of them).
+  const std::uint32_t row_off = static_cast<std::uint32_t>(kv_offset(kv, p0 + (valid ? lane : 0u), g));
+  uint4 pk[16];
+  {
+    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off);
+#pragma unroll
+    for (int w = 0; w < 16; ++w) pk[w] = kr[w];
+  }
+  std::uint32_t vw[kAttnChunk];
+#pragma unroll
+  for (int j = 0; j < static_cast<int>(kAttnChunk); ++j) {
+    const std::uint32_t off = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_off), j));
+    vw[j] = *reinterpret_cast<const std::uint32_t*>(kv.v + off + 2u * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
   float s[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) s[h] = 0.0f;
-  {
-    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off);
-    uint4 pk[16];
 #pragma unroll
-    for (int w = 0; w < 16; ++w) pk[w] = kr[w];
+  for (int w = 0; w < 16; ++w) {
+    const std::uint32_t words[4] = {pk[w].x, pk[w].y, pk[w].z, pk[w].w};
 #pragma unroll
-    for (int w = 0; w < 16; ++w) {
-      const std::uint32_t words[4] = {pk[w].x, pk[w].y, pk[w].z, pk[w].w};
+    for (int e = 0; e < 4; ++e) {
+      const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
+      const int d = 8 * w + 2 * e;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
-        const int d = 8 * w + 2 * e;
-#pragma unroll
-        for (int h = 0; h < GROUP; ++h) s[h] += qg[h * kHeadDim + d] * k0 + qg[h * kHeadDim + d + 1] * k1;
-      }
+      for (int h = 0; h < GROUP; ++h) s[h] += qg[h * kHeadDim + d] * k0 + qg[h * kHeadDim + d + 1] * k1;
     }
   }
   float pw[GROUP], mh[GROUP], lh[GROUP];
@@ -300,30 +323,18 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restric
     lh[h] = wave_sum(pw[h]);
   }
   // o = sum_i p_i v_i over the chunk's 64 positions (weights of invalid ones are
-  // 0 and their rows clamped in range); V rows fetched 16 at a time.
-  const int off_lo = static_cast<int>(row_off & 0xFFFFFFFFu), off_hi = static_cast<int>(row_off >> 32);
+  // 0 and their rows clamped in range).
   float o0[GROUP], o1[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
 #pragma unroll
-  for (int i0 = 0; i0 < static_cast<int>(kAttnChunk); i0 += 16) {
-    std::uint32_t vw[16];
+  for (int j = 0; j < static_cast<int>(kAttnChunk); ++j) {
+    const float v0 = h2f(vw[j]), v1 = h2f(vw[j] >> 16);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const std::size_t off = (static_cast<std::size_t>(static_cast<std::uint32_t>(
-                                   __builtin_amdgcn_readlane(off_hi, i0 + j))) << 32) |
-                              static_cast<std::uint32_t>(__builtin_amdgcn_readlane(off_lo, i0 + j));
-      vw[j] = *reinterpret_cast<const std::uint32_t*>(kv.v + off + 2u * lane);
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float v0 = h2f(vw[j]), v1 = h2f(vw[j] >> 16);
-#pragma unroll
-      for (int h = 0; h < GROUP; ++h) {
-        const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), i0 + j));
-        o0[h] += p * v0;
-        o1[h] += p * v1;
-      }
+    for (int h = 0; h < GROUP; ++h) {
+      const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), j));
+      o0[h] += p * v0;
+      o1[h] += p * v1;
     }
   }
 #pragma unroll
@@ -339,9 +350,10 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restric
 
 // One wave per query head: merge the chunk records (m_c, l_c, o_c) of its kv
 // head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c. Per pass of 64
-// chunks, lane c reads chunk c's (m, l) (wave max / sum), then lane = dimension
-// pair accumulates the weighted o_c, the weights taken by readlane; running
-// sums are rescaled when a later pass raises the maximum.
+// chunks every load is issued up front: lane c reads chunk c's (m, l) (wave max
+// / sum) and, as lane = dimension pair, the pass's 64 o_c rows; the weights are
+// taken by readlane. Running sums are rescaled when a later pass raises the
+// maximum.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
                                                           const std::uint32_t* pos_ptr, std::uint32_t capacity,
                                                           std::uint32_t nchunks, float* __restrict__ att) {
@@ -354,33 +366,29 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const float* base = partials + static_cast<std::size_t>(g) * nchunks * stride + hh * (kHeadDim + 2u);
   float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
   for (std::uint32_t c0 = 0; c0 < n; c0 += 64u) {
-    const std::uint32_t c = c0 + lane;
-    const bool ok = c < n;
-    const float m = ok ? base[c * stride] : -INFINITY;
-    const float l = ok ? base[c * stride + 1u] : 0.0f;
+    const std::uint32_t cnt = n - c0 < 64u ? n - c0 : 64u;
+    const std::uint32_t c = c0 + (lane < cnt ? lane : cnt - 1u);
+    const float m_raw = base[c * stride], l_raw = base[c * stride + 1u];
+    float2 ov[64];
+#pragma unroll
+    for (std::uint32_t j = 0; j < 64u; ++j) {
+      const std::uint32_t cj = c0 + (j < cnt ? j : cnt - 1u);
+      ov[j] = *reinterpret_cast<const float2*>(base + cj * stride + 2u + 2u * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of the reductions
+    const bool ok = lane < cnt;
+    const float m = ok ? m_raw : -INFINITY;
     const float Mn = fmaxf(M, wave_max(m));  // finite: chunk 0 always holds position 0
     const float r = expf(M - Mn);            // 0 on the first pass
     L *= r, o0 *= r, o1 *= r;
     const float w = ok ? expf(m - Mn) : 0.0f;
-    L += wave_sum(w * l);
+    L += wave_sum(ok ? w * l_raw : 0.0f);
     M = Mn;
-    const std::uint32_t cnt = n - c0 < 64u ? n - c0 : 64u;
-    for (std::uint32_t j0 = 0; j0 < cnt; j0 += 8u) {
-      float2 ov[8];
 #pragma unroll
-      for (std::uint32_t j = 0; j < 8u; ++j) {
-        const std::uint32_t cj = c0 + (j0 + j < cnt ? j0 + j : cnt - 1u);
-        ov[j] = *reinterpret_cast<const float2*>(base + cj * stride + 2u + 2u * lane);
-      }
-#pragma unroll
-      for (std::uint32_t j = 0; j < 8u; ++j) {
-        const float wj = j0 + j < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                                      __builtin_bit_cast(int, w),
-                                                                      static_cast<int>(j0 + j)))
-                                      : 0.0f;
-        o0 += wj * ov[j].x;
-        o1 += wj * ov[j].y;
-      }
+    for (std::uint32_t j = 0; j < 64u; ++j) {
+      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), static_cast<int>(j)));
+      o0 += wj * ov[j].x;  // wj = 0 for j >= cnt
+      o1 += wj * ov[j].y;
     }
   }
   *reinterpret_cast<float2*>(att + head * kHeadDim + 2u * lane) = make_float2(o0 / L, o1 / L);
@@ -445,8 +453,10 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
 hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                             std::uint32_t max_ctx, float* partials, float* att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
-      kv.capacity > max_ctx)
+      kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u)
     return hipErrorInvalidValue;
+  // element offsets of a layer's K / V cache fit 32 bits
+  if (static_cast<std::uint64_t>(kv.capacity) * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const std::uint32_t group = n_heads / kv.n_kv;
   const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
   const dim3 grid(nchunks, kv.n_kv), block(64);

@@ -19,6 +19,8 @@
 // work). Summation order is fixed, so results are deterministic run to run.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "iq_grids.h"
 #include "xq.h"
@@ -41,21 +43,33 @@ struct XSrc {
   const float* x;
 };
 
-static __constant__ std::uint16_t kIq2sGridDev[1024] = {RTXLLM_IQ2S_GRID_VALUES};
-static __constant__ std::uint32_t kIq3sGridDev[512] = {RTXLLM_IQ3S_GRID_VALUES};
 
-__device__ __forceinline__ u32x4 ldnt16(const std::uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// Weight streams are read through buffer resources: the row's byte offset is a
+// scalar (soffset), the lane's field offset a fixed VGPR (voffset), so a load
+// costs no address arithmetic, and the hardware range check (num_records = the
+// stream's size) turns any access past the end into a zero. Loads are
+// nontemporal (read once per pass). Fields at 2-byte aligned offsets are read
+// with one unaligned dword / dwordx2 load (gfx950 runs in unaligned access mode).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kLoadNT = 2;  // cache policy bits of a buffer load: nt
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* p, std::uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
 }
-__device__ __forceinline__ std::uint32_t ldnt_u16(const std::uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const std::uint16_t*>(p));
+__device__ __forceinline__ std::uint32_t bld_u8(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, kLoadNT);
 }
-__device__ __forceinline__ std::uint32_t ldnt_u8(const std::uint8_t* p) {
-  return __builtin_nontemporal_load(p);
+__device__ __forceinline__ std::uint32_t bld_u16(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, kLoadNT);
 }
-// Four bytes at a 2-byte aligned address.
-__device__ __forceinline__ std::uint32_t ldnt_u32_a2(const std::uint8_t* p) {
-  return ldnt_u16(p) | (ldnt_u16(p + 2) << 16);
+__device__ __forceinline__ std::uint32_t bld_u32(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kLoadNT);
+}
+__device__ __forceinline__ u32x2 bld_u64(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kLoadNT);
+}
+__device__ __forceinline__ u32x4 bld_u128(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT);
 }
 
 constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S; }
@@ -66,44 +80,95 @@ constexpr bool fmt_is_raw_q4k(int f) { return f == RTXLLM_FMT_Q4K_RAW || f == RT
 // magnitude bytes; sign: sign byte -> (M_lo, M_hi, E_lo, E_hi), M = 0xFF in the
 // byte of every set bit, E = M & 0x01. A signed int8 weight is (mag ^ M) + E:
 // magnitudes are >= 1, so the per-byte add never carries.
-struct IqLds {
+// Codebooks as read by the bit-exact dequant path.
+static __constant__ std::uint16_t kIq2sGridDev[1024] = {RTXLLM_IQ2S_GRID_VALUES};
+static __constant__ std::uint32_t kIq3sGridDev[512] = {RTXLLM_IQ3S_GRID_VALUES};
+
+// LDS codebooks of the IQ formats. grid2: IQ2_S entry -> its eight magnitude
+// bytes 2 l + 1; grid3: IQ3_S entry -> four magnitude bytes; sign: sign byte ->
+// (M0, M1, E0, E1), where byte j of M is 0xFF and of E is 1 when value j is
+// negative, so a signed int8 word is (magnitude ^ M) + E (no carries: every
+// magnitude is odd).
+struct IqLds2 {
   uint2 grid2[1024];
+  uint4 sign[256];
+};
+struct IqLds3 {
   std::uint32_t grid3[512];
   uint4 sign[256];
 };
-
-// The workgroup's codebook copy (only IQ instantiations reference it).
 template <int FMT>
-__device__ __forceinline__ IqLds& iq_lds() {
-  __shared__ IqLds t;
-  return t;
-}
+using IqLds = typename std::conditional<FMT == RTXLLM_FMT_IQ2S, IqLds2, IqLds3>::type;
 
-template <int FMT>
-__device__ void iq_lds_build(IqLds& t) {
-  for (std::uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) {
+// The same tables as device-global images, built at compile time, in the LDS
+// layout: a workgroup copies its image with direct global -> LDS loads.
+template <std::size_t N>
+struct IqImage {
+  std::uint32_t w[N];
+};
+constexpr std::uint16_t kIq2sGridSrc[1024] = {RTXLLM_IQ2S_GRID_VALUES};
+constexpr std::uint32_t kIq3sGridSrc[512] = {RTXLLM_IQ3S_GRID_VALUES};
+
+template <std::size_t N>
+constexpr void iq_image_signs(IqImage<N>& im, std::size_t at) {
+  for (std::uint32_t i = 0; i < 256u; ++i) {
     std::uint32_t m0 = 0u, m1 = 0u;
-#pragma unroll
     for (int j = 0; j < 4; ++j) {
       m0 |= ((i >> j) & 1u) ? (0xFFu << (8 * j)) : 0u;
       m1 |= ((i >> (j + 4)) & 1u) ? (0xFFu << (8 * j)) : 0u;
     }
-    t.sign[i] = make_uint4(m0, m1, m0 & 0x01010101u, m1 & 0x01010101u);
+    im.w[at + 4 * i] = m0;
+    im.w[at + 4 * i + 1] = m1;
+    im.w[at + 4 * i + 2] = m0 & 0x01010101u;
+    im.w[at + 4 * i + 3] = m1 & 0x01010101u;
   }
-  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    for (std::uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) {
-      const std::uint32_t w = kIq2sGridDev[i];
-      std::uint32_t lo = 0u, hi = 0u;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        lo |= (2u * ((w >> (2 * j)) & 3u) + 1u) << (8 * j);
-        hi |= (2u * ((w >> (2 * j + 8)) & 3u) + 1u) << (8 * j);
-      }
-      t.grid2[i] = make_uint2(lo, hi);
+}
+constexpr IqImage<3072> iq2s_image() {
+  IqImage<3072> im{};
+  for (std::uint32_t i = 0; i < 1024u; ++i) {
+    const std::uint32_t w = kIq2sGridSrc[i];
+    std::uint32_t lo = 0u, hi = 0u;
+    for (int j = 0; j < 4; ++j) {
+      lo |= (2u * ((w >> (2 * j)) & 3u) + 1u) << (8 * j);
+      hi |= (2u * ((w >> (2 * j + 8)) & 3u) + 1u) << (8 * j);
     }
-  } else {
-    for (std::uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) t.grid3[i] = kIq3sGridDev[i];
+    im.w[2 * i] = lo;
+    im.w[2 * i + 1] = hi;
   }
+  iq_image_signs(im, 2048);
+  return im;
+}
+constexpr IqImage<1536> iq3s_image() {
+  IqImage<1536> im{};
+  for (std::uint32_t i = 0; i < 512u; ++i) im.w[i] = kIq3sGridSrc[i];
+  iq_image_signs(im, 512);
+  return im;
+}
+static_assert(sizeof(IqImage<3072>) == sizeof(IqLds2) && sizeof(IqImage<1536>) == sizeof(IqLds3), "image layout");
+__device__ const IqImage<3072> kIq2sImage = iq2s_image();
+__device__ const IqImage<1536> kIq3sImage = iq3s_image();
+
+// The workgroup's codebook copy (only IQ instantiations reference it).
+template <int FMT>
+__device__ __forceinline__ IqLds<FMT>& iq_lds() {
+  __shared__ IqLds<FMT> t;
+  return t;
+}
+
+// Start the copy of the codebook image into LDS: 16 B per lane, 1 KB per wave
+// instruction, spread over the workgroup's waves. Asynchronous: the caller
+// waits (s_waitcnt + barrier) before the first lookup.
+template <int FMT>
+__device__ __forceinline__ void iq_lds_fetch(IqLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
+  constexpr std::uint32_t kChunks = sizeof(IqLds<FMT>) / 1024u;  // 1 KB per wave instruction
+  static_assert(sizeof(IqLds<FMT>) % 1024u == 0u, "whole wave chunks");
+  const std::uint32_t nw = blockDim.x >> 6;
+  const uint4* src = reinterpret_cast<const uint4*>(FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kIq2sImage)
+                                                                           : static_cast<const void*>(&kIq3sImage));
+  uint4* dst = reinterpret_cast<uint4*>(&t);
+  for (std::uint32_t c = wave; c < kChunks; c += nw)
+    __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
+                                     (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
 }
 
 // ---- per-format unit load + compute ------------------------------------------
@@ -194,45 +259,45 @@ __device__ __forceinline__ void unit_groups(std::uint32_t b, std::uint32_t k, st
 
 // rp / rm: this row's start in the payload / metadata stream (wave-uniform).
 template <int FMT>
-__device__ __forceinline__ void unit_load(const std::uint8_t* rp, const std::uint8_t* rm, const UnitOff& u,
+__device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, const UnitOff& u,
                                           UnitRaw& r) {
   if constexpr (FMT == RTXLLM_FMT_Q5K) {
-    const u32x4 q = ldnt16(rp + u.o[0]);
-    const u32x4 h = ldnt16(rp + u.o[1]);
-    const u32x4 qh = ldnt16(rp + u.o[2]);
+    const u32x4 q = bld_u128(rp, u.o[0], sp);
+    const u32x4 h = bld_u128(rp, u.o[1], sp);
+    const u32x4 qh = bld_u128(rp, u.o[2], sp);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
     r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     r.c[0] = qh.x, r.c[1] = qh.y, r.c[2] = qh.z, r.c[3] = qh.w;
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    r.c[0] = ldnt_u16(rp + u.o[0]);
-    r.a[0] = ldnt_u32_a2(rp + u.o[1]);
-    r.a[1] = ldnt_u32_a2(rp + u.o[2]);
-    r.c[1] = ldnt_u8(rp + u.o[3]);
-    r.c[2] = ldnt_u8(rp + u.o[4]);
+    r.c[0] = bld_u16(rp, u.o[0], sp);
+    r.a[0] = bld_u32(rp, u.o[1], sp);
+    r.a[1] = bld_u32(rp, u.o[2], sp);
+    r.c[1] = bld_u8(rp, u.o[3], sp);
+    r.c[2] = bld_u8(rp, u.o[4], sp);
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    r.c[0] = ldnt_u16(rp + u.o[0]);
-    r.a[0] = ldnt_u32_a2(rp + u.o[1]);
-    r.a[1] = ldnt_u32_a2(rp + u.o[1] + 4u);
-    r.a[2] = ldnt_u32_a2(rp + u.o[2]);
-    r.c[1] = ldnt_u8(rp + u.o[3]);
-    r.c[2] = ldnt_u8(rp + u.o[4]);
+    r.c[0] = bld_u16(rp, u.o[0], sp);
+    const u32x2 q = bld_u64(rp, u.o[1], sp);
+    r.a[0] = q.x, r.a[1] = q.y;
+    r.a[2] = bld_u32(rp, u.o[2], sp);
+    r.c[1] = bld_u8(rp, u.o[3], sp);
+    r.c[2] = bld_u8(rp, u.o[4], sp);
   } else {
-    const u32x4 q = ldnt16(rp + u.o[0]);
+    const u32x4 q = bld_u128(rp, u.o[0], sp);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
     if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) {
-      const u32x4 h = ldnt16(rp + u.o[1]);
+      const u32x4 h = bld_u128(rp, u.o[1], sp);
       r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE || FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED ||
                          FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
-      const u32x4 h = ldnt16(rm + u.o[1]);
+      const u32x4 h = bld_u128(rm, u.o[1], sm);
       r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
-      const u32x2 h = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rm + u.o[1]));
+      const u32x2 h = bld_u64(rm, u.o[1], sm);
       r.b[0] = h.x, r.b[1] = h.y;
     } else {  // split-compact: f16 d, f16 dmin, u8 sc[8], u8 m[8]
-      r.b[0] = __builtin_nontemporal_load(reinterpret_cast<const std::uint32_t*>(rm + u.o[1]));
-      r.b[1] = ldnt_u16(rm + u.o[2]);
-      r.b[2] = ldnt_u16(rm + u.o[3]);
+      r.b[0] = bld_u32(rm, u.o[1], sm);
+      r.b[1] = bld_u16(rm, u.o[2], sm);
+      r.b[2] = bld_u16(rm, u.o[3], sm);
     }
   }
 }
@@ -259,7 +324,7 @@ __device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uin
 
 template <int FMT>
 __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u, std::uint32_t k, const XG& x0,
-                                              const XG& x1, const IqLds* t) {
+                                              const XG& x1, const IqLds<FMT>* t) {
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
     int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
 #pragma unroll
@@ -418,20 +483,43 @@ __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane
 
 constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slots)
 
+// Rows per epilogue group: epilogues that declare kGroupRows (a multiple of
+// their tile) receive the results of kGroupRows consecutive rows at once.
+template <class E, class = void>
+struct EpiGroupRows {
+  static constexpr std::uint32_t value = 0;
+};
+template <class E>
+struct EpiGroupRows<E, std::void_t<decltype(E::kGroupRows)>> {
+  static constexpr std::uint32_t value = E::kGroupRows;
+};
+
 // UPL units (32 columns each) per lane; a row's `cols / 32` units are split over
 // ks waves of one workgroup, which also holds nrg row groups (blockDim.x = 64 *
-// ks * nrg, ks * nrg <= 8). Row group rg of workgroup b handles tiles b + G *
-// (rg + nrg * j), j = 0, 1, ... (G = gridDim.x), so tiles spread evenly over
-// the CUs, and loads the next tile's rows before it computes the current one.
+// ks * nrg, ks * nrg <= 8). Each row group loads the next tile's rows before it
+// computes the current one. Tile schedule:
+//  * plain epilogues: row group rg of workgroup b handles tiles b + G * (rg +
+//    nrg * j), j = 0, 1, ... (G = gridDim.x), so tiles spread evenly over the
+//    CUs; the epilogue wave of the row group gets each tile's results;
+//  * grouped epilogues (kGroupRows = GR): workgroup b owns the GR-row groups
+//    b + G j; the GR / TILE tiles of a group are spread over the nrg row groups
+//    and R = GR / (TILE nrg) consecutive rounds (the host picks nrg dividing
+//    GR / TILE). Results collect in LDS, and after the group's last round wave 0
+//    hands all GR of them to epi.group(), inside the workgroup: no other
+//    workgroup's results are needed, so no device-wide synchronisation.
 template <int FMT, int UPL, int TILE, bool SELF, class Epi>
 __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows, std::uint32_t ks,
                                                   Epi epi_arg) {
   static_assert(Epi::kTile == TILE, "epilogue tile");
+  constexpr std::uint32_t GR = EpiGroupRows<Epi>::value;
+  static_assert(GR % TILE == 0u, "epilogue group of whole tiles");
+  constexpr std::uint32_t TG = GR > 0u ? GR / TILE : 1u;  // tiles per group
   Epi epi = epi_arg;
-  epi.init(threadIdx.x & 63u);
   // Column-split partials, one slot per wave, double buffered by round parity
   // so a fast wave cannot overwrite a slot another wave still reads.
   __shared__ float part[2][kMaxKs][TILE];
+  // Grouped epilogues: a group's results, double buffered by group parity.
+  __shared__ float gbuf[2][GR > 0u ? GR : 1u];
   const std::uint32_t lane = threadIdx.x & 63u;
   // Wave-uniform values live in SGPRs: row bases become scalar and every load
   // is (scalar row base + per-lane offset).
@@ -439,19 +527,69 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   const std::uint32_t kw = wave % ks, rg = wave / ks, nrg = (blockDim.x >> 6) / ks;
   const std::uint32_t units = w.cols >> 5, bpr = w.cols >> 8;
 
-  std::uint32_t uk[UPL];
+  std::uint32_t uk[UPL], ub[UPL];
+  bool uvalid[UPL];
   UnitOff off[UPL];
-  XG x0[UPL], x1[UPL];
 #pragma unroll
   for (int i = 0; i < UPL; ++i) {
     std::uint32_t u = (kw * UPL + i) * 64u + lane;
-    const bool valid = u < units;
-    u = valid ? u : units - 1u;
-    const std::uint32_t ub = u >> 3;
+    uvalid[i] = u < units;
+    u = uvalid[i] ? u : units - 1u;
+    ub[i] = u >> 3;
     uk[i] = u & 7u;
-    off[i] = unit_offsets<FMT>(ub, uk[i]);
+    off[i] = unit_offsets<FMT>(ub[i], uk[i]);
+  }
+
+  // Row strides and stream sizes in bytes (the host keeps every stream under
+  // 4 GiB).
+  const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
+  const Rsrc rsp = make_rsrc(w.payload, rows * prow);
+  const Rsrc rsm = make_rsrc(FmtBytes<FMT>::meta > 0u ? w.meta : w.payload, rows * mrow);
+  const std::uint32_t tiles = (rows + TILE - 1) / TILE;
+  const std::uint32_t per_round = gridDim.x * nrg;
+  // grouped: rounds per group R = TG / nrg (a power of two), R = 1 << rshift
+  const std::uint32_t rshift = GR > 0u ? static_cast<std::uint32_t>(__builtin_ctz(TG / nrg)) : 0u;
+  const std::uint32_t groups = (tiles + TG - 1u) / TG;
+  const std::uint32_t rounds = GR > 0u ? ((groups + gridDim.x - 1u) / gridDim.x) << rshift
+                                       : (tiles + per_round - 1) / per_round;
+  // tile of round s (>= tiles once s >= rounds)
+  auto tile_of = [&](std::uint32_t s) -> std::uint32_t {
+    if constexpr (GR > 0u) {
+      const std::uint32_t group = blockIdx.x + (s >> rshift) * gridDim.x;
+      return group * TG + ((s & ((1u << rshift) - 1u)) * nrg + rg);
+    } else {
+      return s * per_round + rg * gridDim.x + blockIdx.x;
+    }
+  };
+
+  auto load_tile = [&](std::uint32_t t, UnitRaw (&raw)[TILE][UPL]) {
+    // t is wave-uniform; saying so keeps the row bases in SGPRs in every round
+    t = __builtin_amdgcn_readfirstlane(t);
+    if (t >= tiles) return;
+#pragma unroll
+    for (int rr = 0; rr < TILE; ++rr) {
+      std::uint32_t row = t * TILE + rr;
+      row = row < rows ? row : rows - 1u;
+#pragma unroll
+      for (int i = 0; i < UPL; ++i) unit_load<FMT>(rsp, rsm, row * prow, row * mrow, off[i], raw[rr][i]);
+    }
+  };
+
+  // Prologue, ordered so that loads complete in issue order: the epilogue's
+  // set-up (small, waited for at once), the codebook copy into LDS, the staged
+  // activation, then the first tile's weights; the first wait that needs the
+  // codebook leaves the weights in flight.
+  epi.init(lane);
+  IqLds<FMT>* tables = nullptr;
+  if constexpr (fmt_is_iq(FMT)) {
+    tables = &iq_lds<FMT>();
+    iq_lds_fetch<FMT>(*tables, wave, lane);
+  }
+  XG x0[UPL], x1[UPL];
+#pragma unroll
+  for (int i = 0; i < UPL; ++i) {
     std::uint32_t g0, g1;
-    unit_groups<FMT>(ub, uk[i], g0, g1);
+    unit_groups<FMT>(ub[i], uk[i], g0, g1);
     if constexpr (SELF) {
       xg_stage(xs.x, nullptr, g0, x0[i]);
       xg_stage(xs.x, nullptr, g1, x1[i]);
@@ -459,36 +597,12 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       xg_load(xs.xq, g0, x0[i]);
       xg_load(xs.xq, g1, x1[i]);
     }
-    if (!valid) {
-      xg_zero(x0[i]);
-      xg_zero(x1[i]);
-    }
   }
-  const IqLds* tables = nullptr;
-  if constexpr (fmt_is_iq(FMT)) {
-    IqLds& t = iq_lds<FMT>();
-    iq_lds_build<FMT>(t);
-    __syncthreads();
-    tables = &t;
-  }
+  UnitRaw ra[TILE][UPL], rb[TILE][UPL];
+  load_tile(tile_of(0u), ra);
+  if constexpr (fmt_is_iq(FMT)) __syncthreads();
 
-  const std::size_t prow = static_cast<std::size_t>(bpr) * FmtBytes<FMT>::payload;
-  const std::size_t mrow = static_cast<std::size_t>(bpr) * FmtBytes<FMT>::meta;
-  const std::uint32_t tiles = (rows + TILE - 1) / TILE;
-  const std::uint32_t per_round = gridDim.x * nrg;
-  const std::uint32_t rounds = (tiles + per_round - 1) / per_round;
-
-  auto load_tile = [&](std::uint32_t t, UnitRaw (&raw)[TILE][UPL]) {
-    if (t >= tiles) return;
-#pragma unroll
-    for (int rr = 0; rr < TILE; ++rr) {
-      std::uint32_t row = t * TILE + rr;
-      row = row < rows ? row : rows - 1u;
-#pragma unroll
-      for (int i = 0; i < UPL; ++i) unit_load<FMT>(w.payload + row * prow, w.meta + row * mrow, off[i], raw[rr][i]);
-    }
-  };
-  auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, const UnitRaw (&raw)[TILE][UPL]) {
+  auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, std::uint32_t gpar, const UnitRaw (&raw)[TILE][UPL]) {
     // Every wave of the workgroup runs the same rounds, so the barrier below is
     // uniform; waves without a tile this round still take part in it.
     const bool active = t < tiles;
@@ -498,7 +612,11 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       acc[rr] = 0.0f;
       if (active) {
 #pragma unroll
-        for (int i = 0; i < UPL; ++i) acc[rr] += unit_compute<FMT>(raw[rr][i], off[i], uk[i], x0[i], x1[i], tables);
+        for (int i = 0; i < UPL; ++i) {
+          // a lane past the row's last unit computes a clamped copy and adds 0
+          const float v = unit_compute<FMT>(raw[rr][i], off[i], uk[i], x0[i], x1[i], tables);
+          acc[rr] += uvalid[i] ? v : 0.0f;
+        }
       }
     }
     float v = tile_reduce<TILE>(acc, lane);
@@ -511,20 +629,32 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       v = part[parity][wave][r];
       for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
     }
-    if (active) epi(t * TILE, v, lane, rows);
+    if constexpr (GR > 0u) {
+      if (active && (lane % spread) == 0u) gbuf[gpar][(t % TG) * TILE + r] = v;
+    } else {
+      if (active) epi(t * TILE, v, lane, rows);
+    }
+  };
+  // After round s: a grouped epilogue's group is complete when s is its last
+  // round. The condition is uniform over the workgroup, so is the barrier.
+  auto group_end = [&](std::uint32_t s) {
+    if constexpr (GR > 0u) {
+      if ((s & ((1u << rshift) - 1u)) != (1u << rshift) - 1u) return;
+      const std::uint32_t group = blockIdx.x + (s >> rshift) * gridDim.x;
+      if (group >= groups) return;
+      __syncthreads();
+      if (wave == 0u) epi.group(group * GR, gbuf[(s >> rshift) & 1u], lane, rows);
+    }
   };
 
-  UnitRaw ra[TILE][UPL], rb[TILE][UPL];
-  std::uint32_t t = rg * gridDim.x + blockIdx.x;
-  load_tile(t, ra);
-  for (std::uint32_t round = 0; round < rounds; round += 2) {
-    load_tile(t + per_round, rb);
-    finish_tile(t, 0u, ra);
-    t += per_round;
-    if (round + 1 >= rounds) break;
-    load_tile(t + per_round, ra);
-    finish_tile(t, 1u, rb);
-    t += per_round;
+  for (std::uint32_t s = 0; s < rounds; s += 2u) {
+    load_tile(tile_of(s + 1u), rb);
+    finish_tile(tile_of(s), 0u, (s >> rshift) & 1u, ra);
+    group_end(s);
+    if (s + 1u >= rounds) break;
+    load_tile(tile_of(s + 2u), ra);
+    finish_tile(tile_of(s + 1u), 1u, ((s + 1u) >> rshift) & 1u, rb);
+    group_end(s + 1u);
   }
 }
 

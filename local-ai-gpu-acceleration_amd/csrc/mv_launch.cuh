@@ -19,25 +19,45 @@ inline int num_cus() {
   return cached;
 }
 
-// Launch geometry of mv_kernel, from a sweep on MI355X at the 8B shapes: one
-// unit (32 columns) per lane for rows of up to 16384 columns (two beyond),
-// ks = ceil(units / 64) waves per row, nrg = 4 / ks row groups per workgroup
-// (at least 1), and one 4-row tile per row group: many small workgroups keep
-// enough loads in flight and the dispatcher's tail short.
+// Launch geometry of mv_kernel, from sweeps on MI355X at the 8B decode shapes:
+//  * one unit (32 columns) per lane for rows of up to 16384 columns (two
+//    beyond), ks = ceil(units / 64) waves per row;
+//  * small matrices: nrg = 4 / ks row groups per workgroup (at least 1) and one
+//    4-row tile per row group: many small workgroups, every tile in flight;
+//  * large matrices (more waves than fit the chip at once): persistent row
+//    groups, nrg = 1 and at most 16 waves per CU for the IQ formats (their
+//    LDS decode is latency bound, so more waves help) and 8 per CU for the
+//    K-quants; each wave double-buffers its tiles and builds its codebook once.
+//  * grouped epilogues (group_rows > 0): one group per workgroup, its tiles
+//    over as many row groups as fit in 8 waves (nrg divides the group's tile
+//    count) and the rest over consecutive rounds.
 struct MvGeom {
   int upl;
   unsigned ks, nrg, grid;
 };
 
-inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, MvGeom& g) {
-  (void)fmt;
+inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, std::uint32_t group_rows, MvGeom& g) {
   const std::uint32_t units = cols / 32u;
   g.upl = units > 512u ? 2 : 1;
   g.ks = (units + 64u * g.upl - 1u) / (64u * g.upl);
   if (g.ks > static_cast<unsigned>(kMaxKs)) return false;
-  g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
   const std::uint32_t tiles = (rows + tile - 1) / tile;
-  const std::uint32_t grid = (tiles + g.nrg - 1) / g.nrg;
+  std::uint32_t grid;
+  if (group_rows > 0u) {
+    const std::uint32_t tg = group_rows / static_cast<std::uint32_t>(tile);
+    g.nrg = 1u;
+    while (2u * g.nrg <= tg && tg % (2u * g.nrg) == 0u && g.ks * 2u * g.nrg <= static_cast<unsigned>(kMaxKs))
+      g.nrg *= 2u;
+    grid = (tiles + tg - 1u) / tg;
+  } else {
+    const std::uint32_t max_waves = (fmt_is_iq(fmt) ? 16u : 8u) * static_cast<std::uint32_t>(num_cus());
+    g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
+    grid = (tiles + g.nrg - 1) / g.nrg;
+    if (static_cast<std::uint64_t>(grid) * g.ks * g.nrg > max_waves) {
+      g.nrg = 1u;
+      grid = max_waves / g.ks;
+    }
+  }
   g.grid = grid < 1u ? 1u : (grid > 1048576u ? 1048576u : grid);
   return true;
 }
@@ -46,8 +66,12 @@ template <int FMT, bool SELF, class Epi>
 inline hipError_t launch_mv_fmt(const QTensor& w, const XSrc& xs, std::uint32_t row_count, const Epi& epi,
                          hipStream_t stream) {
   constexpr int kT = Epi::kTile;
+  // the kernel addresses each stream with 32-bit byte offsets
+  const std::uint64_t blocks = static_cast<std::uint64_t>(row_count) * (w.cols / 256u);
+  if (blocks * FmtBytes<FMT>::payload > 0xFFFFFFFFull || blocks * FmtBytes<FMT>::meta > 0xFFFFFFFFull)
+    return hipErrorInvalidValue;
   MvGeom g;
-  if (!mv_geom(FMT, row_count, w.cols, kT, g)) return hipErrorInvalidValue;
+  if (!mv_geom(FMT, row_count, w.cols, kT, EpiGroupRows<Epi>::value, g)) return hipErrorInvalidValue;
   const dim3 grid(g.grid), block(64u * g.ks * g.nrg);
   if (g.upl == 2) {
     hipLaunchKernelGGL((mv_kernel<FMT, 2, kT, SELF, Epi>), grid, block, 0, stream, w, xs, row_count, g.ks, epi);
