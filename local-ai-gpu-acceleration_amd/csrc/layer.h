@@ -49,32 +49,36 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
                       const std::uint32_t* pos, float* q_out, const KvLayer& kv, hipStream_t stream);
 
 // GQA decode attention over positions [0, *pos] of the paged cache: split over
-// context chunks (partials) then combined into att[n_heads * head_dim].
+// context chunks (partials) then combined into att[n_heads * head_dim], which
+// is also staged (16-value groups) into xq_att for the o projection.
 hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                            std::uint32_t max_ctx, float* partials, float* att, hipStream_t stream);
+                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream);
 std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx);
 
-// h += W x (rows % 16 == 0) with x = fp32 x_in staged per wave; then xq_next =
+// h += W x (rows % 16 == 0), x either the staged input xq_in or the fp32 x_in
+// (staged by each wave itself; exactly one of the two non-null); then xq_next =
 // stage(h * w_next), sumsq_next[t] = sum of h^2 over rows [16 t, 16 t + 16).
 hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                           std::uint32_t cols, const float* x_in, float* h, const float* w_next, void* xq_next,
-                           float* sumsq_next, hipStream_t stream);
+                           std::uint32_t cols, const void* xq_in, const float* x_in, float* h, const float* w_next,
+                           void* xq_next, float* sumsq_next, hipStream_t stream);
 
 // Rows interleaved gate / up (row 2i = gate_i, row 2i + 1 = up_i), x =
 // rmsnorm(h): act[i] = silu(gate_i) * up_i.
 hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
                           std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream);
 
-// logits = W rmsnorm(h); argkey = max over rows of (ordered(logit) << 32 | ~row)
-// (greedy argmax, lowest index on ties, NaN never wins). argkey must be 0 before.
+// logits = W rmsnorm(h), and per row group of the launch the best argmax key
+// (ordered(logit) << 32 | ~row: greedy argmax, lowest index on ties, NaN never
+// wins) in keys[0, *key_count); logits_key_slots() is that count (the launch
+// fails if it exceeds key_capacity).
+std::uint32_t logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols);
 hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* argkey,
-                         hipStream_t stream);
+                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* keys,
+                         std::uint32_t key_capacity, std::uint32_t* key_count, hipStream_t stream);
 
-// token[0] = argmax from argkey (0 if every logit was NaN); *pos += advance;
-// argkey = 0.
-hipError_t launch_argmax_finalize(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
-                                  std::uint32_t advance, hipStream_t stream);
+// token[0] = argmax over keys[0, count) (0 if every logit was NaN); *pos += advance.
+hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
+                                  std::uint32_t* pos, std::uint32_t advance, hipStream_t stream);
 
 // Device-side synthetic packs, bit-identical to the host generator
 // (rtxllm_synth_raw_blocks): raw blocks of format 0/5/6/7, or the Q4_K

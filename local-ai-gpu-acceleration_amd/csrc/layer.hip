@@ -70,6 +70,32 @@ __device__ __forceinline__ std::uint16_t f2h(float v) {
   return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
 }
 
+// Stage one 16-value group held by the 16 lanes with owner = true (lane i of
+// them holds value x of index `idx`; non-owners pass x = 0): the quant16 rule,
+// evaluated with wave reductions (max and integer sum are order independent,
+// so the digits equal quant16's). g0 = first index of the group.
+__device__ __forceinline__ void stage_group16(const XQOut& xq, std::uint32_t g0, std::uint32_t idx, float x,
+                                              bool owner, std::uint32_t lane) {
+  const float m = wave_max(fabsf(x));
+  const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
+  const float s = m / kXQLimitF;
+  int X = static_cast<int>(rintf(x * inv));
+  X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
+  int H, M, L;
+  xq_digits(X, H, M, L);
+  const int total = wave_sum_i(owner ? X : 0);
+  if (owner) {
+    xq.h[idx] = static_cast<std::int8_t>(H);
+    xq.m[idx] = static_cast<std::int8_t>(M);
+    xq.l[idx] = static_cast<std::int8_t>(L);
+  }
+  if (lane == 0u) {
+    const std::uint32_t t = g0 / kXGroup;
+    xq.s[t] = s;
+    xq.sum[t] = s * static_cast<float>(total);
+  }
+}
+
 // ---- epilogues (TILE 4: row r of a tile in lanes [16 r, 16 r + 16)) ---------
 
 struct EpiQkv {
@@ -137,16 +163,24 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, std::uint32_t 
   return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - row);
 }
 
+// Logits and the greedy argmax: each row group keeps the best key of its tiles
+// in a register and stores it once, after its last tile, into its own slot;
+// the finalize kernel reduces the slots (no atomics, no per-tile reads).
 struct EpiLogits {
   static constexpr int kTile = 4;
+  static constexpr bool kFinish = true;
   const float* sumsq;
   std::uint32_t nslots, n;
   float eps;
   float* logits;
-  unsigned long long* argkey;
+  unsigned long long* keys;
   float scale;
-  __device__ __forceinline__ void init(std::uint32_t lane) { scale = inv_rms(sumsq, nslots, n, eps, lane); }
-  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
+  unsigned long long best;
+  __device__ __forceinline__ void init(std::uint32_t lane) {
+    scale = inv_rms(sumsq, nslots, n, eps, lane);
+    best = 0ull;
+  }
+  __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) {
     const std::uint32_t row = row0 + (lane >> 4);
     const float y = v * scale;
     const bool ok = row < rows;
@@ -155,10 +189,11 @@ struct EpiLogits {
     unsigned long long other = __shfl_xor(key, 16, 64);
     key = other > key ? other : key;
     other = __shfl_xor(key, 32, 64);
-    key = other > key ? other : key;
-    // Most tiles lose to the running maximum: read it first (a plain L2 read)
-    // and only then contend for the atomic.
-    if (lane == 0u && key != 0ull && key > __builtin_nontemporal_load(argkey)) atomicMax(argkey, key);
+    key = other > key ? other : key;  // every lane: the tile's best
+    best = key > best ? key : best;
+  }
+  __device__ __forceinline__ void finish(std::uint32_t slot, std::uint32_t lane) const {
+    if (lane == 0u) keys[slot] = best;
   }
 };
 
@@ -179,27 +214,10 @@ struct EpiResidual {
     const float hn = h[row] + (owner ? vals[lane] : 0.0f);
     if (owner) h[row] = hn;
     const float sq = wave_sum(owner ? hn * hn : 0.0f);
-    // stage the 16-value group h * w_next exactly as quant16 does
+    // stage the 16-value group h * w_next
     const float x = owner ? (w_next != nullptr ? hn * w_next[row] : hn) : 0.0f;
-    const float m = wave_max(fabsf(x));
-    const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
-    const float s = m / kXQLimitF;
-    int X = static_cast<int>(rintf(x * inv));
-    X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
-    int H, M, L;
-    xq_digits(X, H, M, L);
-    const int total = wave_sum_i(owner ? X : 0);
-    if (owner) {
-      xq.h[row] = static_cast<std::int8_t>(H);
-      xq.m[row] = static_cast<std::int8_t>(M);
-      xq.l[row] = static_cast<std::int8_t>(L);
-    }
-    if (lane == 0u) {
-      const std::uint32_t t = row0 / kXGroup;
-      xq.s[t] = s;
-      xq.sum[t] = s * static_cast<float>(total);
-      sumsq[t] = sq;
-    }
+    stage_group16(xq, row0, row, x, owner, lane);
+    if (lane == 0u) sumsq[row0 / kXGroup] = sq;
   }
 };
 
@@ -356,7 +374,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restric
 // maximum.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
                                                           const std::uint32_t* pos_ptr, std::uint32_t capacity,
-                                                          std::uint32_t nchunks, float* __restrict__ att) {
+                                                          std::uint32_t nchunks, float* __restrict__ att, XQOut xq) {
   const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
   const std::uint32_t g = head / group, hh = head % group;
   const std::uint32_t pos = *pos_ptr < capacity ? *pos_ptr : capacity - 1u;
@@ -391,16 +409,60 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
       o1 += wj * ov[j].y;
     }
   }
-  *reinterpret_cast<float2*>(att + head * kHeadDim + 2u * lane) = make_float2(o0 / L, o1 / L);
+  const float a0 = o0 / L, a1 = o1 / L;
+  const std::uint32_t d0 = head * kHeadDim + 2u * lane;
+  *reinterpret_cast<float2*>(att + d0) = make_float2(a0, a1);
+  // Stage att for the o projection: the 16-value group of dims [16 k, 16 k + 16)
+  // is held by lanes [8 k, 8 k + 8), two values each (the quant16 rule; max and
+  // integer sum are order independent, so the digits equal quant16's).
+  float m = fmaxf(fabsf(a0), fabsf(a1));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  m = fmaxf(m, __shfl_xor(m, 4, 64));
+  const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
+  const float s = m / kXQLimitF;
+  int X0 = static_cast<int>(rintf(a0 * inv)), X1 = static_cast<int>(rintf(a1 * inv));
+  X0 = X0 > kXQLimit ? kXQLimit : (X0 < -kXQLimit ? -kXQLimit : X0);
+  X1 = X1 > kXQLimit ? kXQLimit : (X1 < -kXQLimit ? -kXQLimit : X1);
+  int H0, M0, L0, H1, M1, L1;
+  xq_digits(X0, H0, M0, L0);
+  xq_digits(X1, H1, M1, L1);
+  int total = X0 + X1;
+  total += __shfl_xor(total, 1, 64);
+  total += __shfl_xor(total, 2, 64);
+  total += __shfl_xor(total, 4, 64);
+  auto pair = [](int lo, int hi) {
+    return static_cast<std::uint16_t>((static_cast<std::uint32_t>(lo) & 0xFFu) |
+                                      ((static_cast<std::uint32_t>(hi) & 0xFFu) << 8));
+  };
+  *reinterpret_cast<std::uint16_t*>(xq.h + d0) = pair(H0, H1);
+  *reinterpret_cast<std::uint16_t*>(xq.m + d0) = pair(M0, M1);
+  *reinterpret_cast<std::uint16_t*>(xq.l + d0) = pair(L0, L1);
+  if ((lane & 7u) == 0u) {
+    const std::uint32_t t = d0 / kXGroup;
+    xq.s[t] = s;
+    xq.sum[t] = s * static_cast<float>(total);
+  }
 }
 
-__global__ void argmax_finalize_kernel(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
-                                       std::uint32_t advance) {
+// One workgroup of 256: the maximum of count keys, then token and position.
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
+                                                              std::uint32_t count, std::uint32_t* token,
+                                                              std::uint32_t* pos, std::uint32_t advance) {
+  __shared__ unsigned long long part[4];
+  unsigned long long best = 0ull;
+  for (std::uint32_t i = threadIdx.x; i < count; i += 256u) best = keys[i] > best ? keys[i] : best;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long other = __shfl_xor(best, o, 64);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = best;
+  __syncthreads();
   if (threadIdx.x != 0u) return;
-  const unsigned long long key = *argkey;
-  token[0] = key == 0ull ? 0u : 0xFFFFFFFFu - static_cast<std::uint32_t>(key & 0xFFFFFFFFull);
+  for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
+  token[0] = best == 0ull ? 0u : 0xFFFFFFFFu - static_cast<std::uint32_t>(best & 0xFFFFFFFFull);
   if (pos != nullptr) pos[0] += advance;
-  *argkey = 0ull;
 }
 
 // ---- device-side synthetic packs ------------------------------------------------
@@ -451,7 +513,7 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
 }
 
 hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                            std::uint32_t max_ctx, float* partials, float* att, hipStream_t stream) {
+                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
       kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u)
     return hipErrorInvalidValue;
@@ -469,17 +531,19 @@ hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_h
   }
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
+  if (xq_att == nullptr) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, partials, group, pos, kv.capacity,
-                     nchunks, att);
+                     nchunks, att, xq_out(xq_att, n_heads * kHeadDim));
   return hipGetLastError();
 }
 
 hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                           std::uint32_t cols, const float* x_in, float* h, const float* w_next, void* xq_next,
-                           float* sumsq_next, hipStream_t stream) {
-  if ((rows % kXGroup) != 0u) return hipErrorInvalidValue;
+                           std::uint32_t cols, const void* xq_in, const float* x_in, float* h, const float* w_next,
+                           void* xq_next, float* sumsq_next, hipStream_t stream) {
+  if ((rows % kXGroup) != 0u || (xq_in == nullptr) == (x_in == nullptr)) return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   const EpiResidual e{h, w_next, xq_out(xq_next, rows), sumsq_next};
+  if (xq_in != nullptr) return launch_mv<false>(fmt, w, XSrc{xq_view(xq_in, cols), nullptr}, rows, e, stream);
   return launch_mv<true>(fmt, w, XSrc{XQ{}, x_in}, rows, e, stream);
 }
 
@@ -492,18 +556,27 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
   return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
 }
 
+std::uint32_t logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols) {
+  MvGeom g;
+  if (!mv_geom(fmt, rows, cols, EpiLogits::kTile, 0u, g)) return 0u;
+  return g.grid * g.nrg;
+}
+
 hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* argkey,
-                         hipStream_t stream) {
+                         std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* keys,
+                         std::uint32_t key_capacity, std::uint32_t* key_count, hipStream_t stream) {
+  const std::uint32_t slots = logits_key_slots(fmt, rows, cols);
+  if (slots == 0u || slots > key_capacity || keys == nullptr) return hipErrorInvalidValue;
+  if (key_count != nullptr) *key_count = slots;
   const QTensor w{payload, meta, rows, cols};
   EpiLogits e{};
-  e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.logits = logits, e.argkey = argkey;
+  e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.logits = logits, e.keys = keys;
   return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
 }
 
-hipError_t launch_argmax_finalize(unsigned long long* argkey, std::uint32_t* token, std::uint32_t* pos,
-                                  std::uint32_t advance, hipStream_t stream) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(64), 0, stream, argkey, token, pos, advance);
+hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
+                                  std::uint32_t* pos, std::uint32_t advance, hipStream_t stream) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, count, token, pos, advance);
   return hipGetLastError();
 }
 

@@ -25,6 +25,7 @@ struct rtxllm_llama {
   rtxllm::VramSuperallocator arena;
   rtxllm::HipGraphBucket graph;
   std::uint32_t q_rows = 0, kv_rows = 0, nslots = 0;
+  std::uint32_t key_slots = 0;  // argmax slots of the LM-head launch
   std::size_t partial_floats = 0;
 };
 
@@ -136,10 +137,12 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   specs.push_back({"sumsq", 4u * m->nslots});
   specs.push_back({"q", 4u * m->q_rows});
   specs.push_back({"att", 4u * m->q_rows});
+  specs.push_back({"xq_att", rtxllm::xq_bytes(m->q_rows)});
   specs.push_back({"attn_partials", 4u * m->partial_floats});
   specs.push_back({"act", 4u * c.ffn});
   specs.push_back({"logits", 4u * c.vocab});
-  specs.push_back({"argkey", 8u});
+  m->key_slots = rtxllm::logits_key_slots(c.fmt_lm_head, c.vocab, c.hidden);
+  specs.push_back({"argkeys", 8u * (m->key_slots > 0u ? m->key_slots : 1u)});
   specs.push_back({"token", 4u});
   specs.push_back({"pos", 4u});
   specs.push_back({"inv_freq", 4u * rtxllm::kHeadDim / 2u});
@@ -245,10 +248,12 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
     }
     case kAttention:
       return rtxllm::launch_attention(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
-                                      region<float>(m, "attn_partials"), region<float>(m, "att"), stream);
+                                      region<float>(m, "attn_partials"), region<float>(m, "att"),
+                                      m->arena.arena_ptr("xq_att"), stream);
     case kO: {
       const TensorRef t = tensor(m, layer_name("o", l));
-      return rtxllm::launch_residual(c.fmt_o, t.payload, t.meta, c.hidden, m->q_rows, region<float>(m, "att"), h,
+      return rtxllm::launch_residual(c.fmt_o, t.payload, t.meta, c.hidden, m->q_rows, m->arena.arena_ptr("xq_att"),
+                                     nullptr, h,
                                      region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
     }
     case kGateUp: {
@@ -258,16 +263,17 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
     }
     case kDown: {
       const TensorRef t = tensor(m, layer_name("down", l));
-      return rtxllm::launch_residual(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, region<float>(m, "act"), h,
+      return rtxllm::launch_residual(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, nullptr, region<float>(m, "act"), h,
                                      next_norm, xq, sumsq, stream);
     }
     case kHead: {
       const TensorRef t = tensor(m, "lm_head");
-      auto* argkey = region<unsigned long long>(m, "argkey");
+      auto* keys = region<unsigned long long>(m, "argkeys");
+      std::uint32_t count = 0u;
       const hipError_t st = rtxllm::launch_logits(c.fmt_lm_head, t.payload, t.meta, c.vocab, c.hidden, in,
-                                                  region<float>(m, "logits"), argkey, stream);
+                                                  region<float>(m, "logits"), keys, m->key_slots, &count, stream);
       if (st != hipSuccess) return st;
-      return rtxllm::launch_argmax_finalize(argkey, region<std::uint32_t>(m, "token"), pos, 1u, stream);
+      return rtxllm::launch_argmax_finalize(keys, count, region<std::uint32_t>(m, "token"), pos, 1u, stream);
     }
     default: return hipErrorInvalidValue;
   }

@@ -47,32 +47,44 @@ struct XSrc {
 // Weight streams are read through buffer resources: the row's byte offset is a
 // scalar (soffset), the lane's field offset a fixed VGPR (voffset), so a load
 // costs no address arithmetic, and the hardware range check (num_records = the
-// stream's size) turns any access past the end into a zero. Loads are
-// nontemporal (read once per pass). Fields at 2-byte aligned offsets are read
-// with one unaligned dword / dwordx2 load (gfx950 runs in unaligned access mode).
+// stream's size) turns any access past the end into a zero. Fields at 2-byte
+// aligned offsets are read with one unaligned dword / dwordx2 load (gfx950 runs
+// in unaligned access mode). Cache policy per format (measured at the 8B
+// shapes): the Q4_K streams, one 16 B run of quants per lane, are read
+// nontemporal; the IQ and Q5_K blocks are read as several small fields of the
+// same cache lines, which only the L1 turns into one L2 request per line, so
+// those loads keep the default policy.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr int kLoadNT = 2;  // cache policy bits of a buffer load: nt
+constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S; }
+template <int FMT>
+constexpr int load_policy() {
+  return (fmt_is_iq(FMT) || FMT == RTXLLM_FMT_Q5K) ? 0 : 2;  // 2 = nt
+}
 
 __device__ __forceinline__ Rsrc make_rsrc(const void* p, std::uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
 }
+template <int P>
 __device__ __forceinline__ std::uint32_t bld_u8(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, kLoadNT);
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, P);
 }
+template <int P>
 __device__ __forceinline__ std::uint32_t bld_u16(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, kLoadNT);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, P);
 }
+template <int P>
 __device__ __forceinline__ std::uint32_t bld_u32(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kLoadNT);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, P);
 }
+template <int P>
 __device__ __forceinline__ u32x2 bld_u64(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kLoadNT);
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, P);
 }
+template <int P>
 __device__ __forceinline__ u32x4 bld_u128(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, P);
 }
 
-constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S; }
 constexpr bool fmt_is_raw_q4k(int f) { return f == RTXLLM_FMT_Q4K_RAW || f == RTXLLM_FMT_Q4K_RAW_PREDECODED; }
 
 // ---- LDS codebooks for the IQ formats ---------------------------------------
@@ -261,43 +273,44 @@ __device__ __forceinline__ void unit_groups(std::uint32_t b, std::uint32_t k, st
 template <int FMT>
 __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, const UnitOff& u,
                                           UnitRaw& r) {
+  constexpr int P = load_policy<FMT>();
   if constexpr (FMT == RTXLLM_FMT_Q5K) {
-    const u32x4 q = bld_u128(rp, u.o[0], sp);
-    const u32x4 h = bld_u128(rp, u.o[1], sp);
-    const u32x4 qh = bld_u128(rp, u.o[2], sp);
+    const u32x4 q = bld_u128<P>(rp, u.o[0], sp);
+    const u32x4 h = bld_u128<P>(rp, u.o[1], sp);
+    const u32x4 qh = bld_u128<P>(rp, u.o[2], sp);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
     r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     r.c[0] = qh.x, r.c[1] = qh.y, r.c[2] = qh.z, r.c[3] = qh.w;
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    r.c[0] = bld_u16(rp, u.o[0], sp);
-    r.a[0] = bld_u32(rp, u.o[1], sp);
-    r.a[1] = bld_u32(rp, u.o[2], sp);
-    r.c[1] = bld_u8(rp, u.o[3], sp);
-    r.c[2] = bld_u8(rp, u.o[4], sp);
+    r.c[0] = bld_u16<P>(rp, u.o[0], sp);
+    r.a[0] = bld_u32<P>(rp, u.o[1], sp);
+    r.a[1] = bld_u32<P>(rp, u.o[2], sp);
+    r.c[1] = bld_u8<P>(rp, u.o[3], sp);
+    r.c[2] = bld_u8<P>(rp, u.o[4], sp);
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    r.c[0] = bld_u16(rp, u.o[0], sp);
-    const u32x2 q = bld_u64(rp, u.o[1], sp);
+    r.c[0] = bld_u16<P>(rp, u.o[0], sp);
+    const u32x2 q = bld_u64<P>(rp, u.o[1], sp);
     r.a[0] = q.x, r.a[1] = q.y;
-    r.a[2] = bld_u32(rp, u.o[2], sp);
-    r.c[1] = bld_u8(rp, u.o[3], sp);
-    r.c[2] = bld_u8(rp, u.o[4], sp);
+    r.a[2] = bld_u32<P>(rp, u.o[2], sp);
+    r.c[1] = bld_u8<P>(rp, u.o[3], sp);
+    r.c[2] = bld_u8<P>(rp, u.o[4], sp);
   } else {
-    const u32x4 q = bld_u128(rp, u.o[0], sp);
+    const u32x4 q = bld_u128<P>(rp, u.o[0], sp);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
     if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) {
-      const u32x4 h = bld_u128(rp, u.o[1], sp);
+      const u32x4 h = bld_u128<P>(rp, u.o[1], sp);
       r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE || FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED ||
                          FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
-      const u32x4 h = bld_u128(rm, u.o[1], sm);
+      const u32x4 h = bld_u128<P>(rm, u.o[1], sm);
       r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
-      const u32x2 h = bld_u64(rm, u.o[1], sm);
+      const u32x2 h = bld_u64<P>(rm, u.o[1], sm);
       r.b[0] = h.x, r.b[1] = h.y;
     } else {  // split-compact: f16 d, f16 dmin, u8 sc[8], u8 m[8]
-      r.b[0] = bld_u32(rm, u.o[1], sm);
-      r.b[1] = bld_u16(rm, u.o[2], sm);
-      r.b[2] = bld_u16(rm, u.o[3], sm);
+      r.b[0] = bld_u32<P>(rm, u.o[1], sm);
+      r.b[1] = bld_u16<P>(rm, u.o[2], sm);
+      r.b[2] = bld_u16<P>(rm, u.o[3], sm);
     }
   }
 }
@@ -494,6 +507,18 @@ struct EpiGroupRows<E, std::void_t<decltype(E::kGroupRows)>> {
   static constexpr std::uint32_t value = E::kGroupRows;
 };
 
+// Epilogues that declare kFinish get epi.finish(slot, lane) from each row
+// group's epilogue wave after its last tile; slot = blockIdx.x * nrg + rg is
+// unique per row group (< gridDim.x * nrg).
+template <class E, class = void>
+struct EpiHasFinish {
+  static constexpr bool value = false;
+};
+template <class E>
+struct EpiHasFinish<E, std::void_t<decltype(E::kFinish)>> {
+  static constexpr bool value = E::kFinish;
+};
+
 // UPL units (32 columns each) per lane; a row's `cols / 32` units are split over
 // ks waves of one workgroup, which also holds nrg row groups (blockDim.x = 64 *
 // ks * nrg, ks * nrg <= 8). Each row group loads the next tile's rows before it
@@ -655,6 +680,9 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     load_tile(tile_of(s + 2u), ra);
     finish_tile(tile_of(s + 1u), 1u, ((s + 1u) >> rshift) & 1u, rb);
     group_end(s + 1u);
+  }
+  if constexpr (EpiHasFinish<Epi>::value) {
+    if (kw == 0u) epi.finish(blockIdx.x * nrg + rg, lane);
   }
 }
 

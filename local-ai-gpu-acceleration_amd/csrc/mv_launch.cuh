@@ -24,13 +24,13 @@ inline int num_cus() {
 //    beyond), ks = ceil(units / 64) waves per row;
 //  * small matrices: nrg = 4 / ks row groups per workgroup (at least 1) and one
 //    4-row tile per row group: many small workgroups, every tile in flight;
-//  * large matrices (more waves than fit the chip at once): persistent row
-//    groups, nrg = 1 and at most 16 waves per CU for the IQ formats (their
-//    LDS decode is latency bound, so more waves help) and 8 per CU for the
-//    K-quants; each wave double-buffers its tiles and builds its codebook once.
-//  * grouped epilogues (group_rows > 0): one group per workgroup, its tiles
-//    over as many row groups as fit in 8 waves (nrg divides the group's tile
-//    count) and the rest over consecutive rounds.
+//  * large matrices (more than 16 waves per CU): persistent workgroups, the
+//    grid capped at 16 waves per CU; each row group double-buffers its tiles
+//    and the workgroup copies its codebook once.
+//  * grouped epilogues (group_rows > 0): a group's tiles over as many row
+//    groups as fit in 8 waves (nrg divides the group's tile count) and the rest
+//    over consecutive rounds; one group per workgroup, or several in turn when
+//    that would exceed the wave budget above.
 struct MvGeom {
   int upl;
   unsigned ks, nrg, grid;
@@ -43,20 +43,19 @@ inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, s
   if (g.ks > static_cast<unsigned>(kMaxKs)) return false;
   const std::uint32_t tiles = (rows + tile - 1) / tile;
   std::uint32_t grid;
+  const std::uint32_t max_waves = 16u * static_cast<std::uint32_t>(num_cus());
   if (group_rows > 0u) {
     const std::uint32_t tg = group_rows / static_cast<std::uint32_t>(tile);
     g.nrg = 1u;
     while (2u * g.nrg <= tg && tg % (2u * g.nrg) == 0u && g.ks * 2u * g.nrg <= static_cast<unsigned>(kMaxKs))
       g.nrg *= 2u;
     grid = (tiles + tg - 1u) / tg;
+    const std::uint32_t cap = max_waves / (g.ks * g.nrg);
+    if (grid > cap && cap > 0u) grid = cap;  // workgroups take several groups in turn
   } else {
-    const std::uint32_t max_waves = (fmt_is_iq(fmt) ? 16u : 8u) * static_cast<std::uint32_t>(num_cus());
     g.nrg = g.ks >= 4u ? 1u : 4u / g.ks;
     grid = (tiles + g.nrg - 1) / g.nrg;
-    if (static_cast<std::uint64_t>(grid) * g.ks * g.nrg > max_waves) {
-      g.nrg = 1u;
-      grid = max_waves / g.ks;
-    }
+    if (static_cast<std::uint64_t>(grid) * g.ks * g.nrg > max_waves) grid = max_waves / (g.ks * g.nrg);
   }
   g.grid = grid < 1u ? 1u : (grid > 1048576u ? 1048576u : grid);
   return true;
