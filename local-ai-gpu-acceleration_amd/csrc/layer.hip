@@ -270,106 +270,145 @@ __global__ __launch_bounds__(1024) void embed_q5k_kernel(const std::uint8_t* __r
 
 // ---- attention -------------------------------------------------------------------
 
-constexpr std::uint32_t kAttnChunk = 64;  // positions per workgroup (one wave)
+constexpr std::uint32_t kAttnWaves = 8;                // waves per workgroup
+constexpr std::uint32_t kAttnSub = 16;                 // positions per wave
+constexpr std::uint32_t kAttnChunk = kAttnWaves * kAttnSub;  // positions per workgroup
 constexpr std::uint32_t kMaxGroup = 8;
+constexpr std::uint32_t kQPad = kHeadDim / 4u + 1u;    // LDS stride of a quarter of q (bank spread)
 
-// One wave per (chunk c of 64 positions, kv head g): the `GROUP` query heads of
-// g over positions [64 c, 64 c + 64) ∩ [0, pos]. Every K and V load of the chunk
-// is issued up front (32 KB per wave in flight), then:
-//  * scores: lane = position; the lane dots its K row (256 B) with the heads'
-//    q, which every lane reads at the same address (scalar loads, broadcast);
-//  * chunk softmax per head: m = max, p = exp(s - m), l = sum p (wave
-//    reductions);
+// One workgroup of 8 waves per (chunk c of 128 positions, kv head g): the
+// `GROUP` query heads of g over positions [128 c, 128 c + 128) ∩ [0, pos]. Wave
+// w takes positions [128 c + 16 w, +16); all its K and V loads are issued up
+// front. Then:
+//  * scores: lane = (position 0..15, quarter of the head dims); the lane dots
+//    its 32 dims of the K row with the heads' q (from LDS, broadcast within a
+//    quarter) and two xor-shuffles sum the quarters;
+//  * wave softmax per head: m = max, p = exp(s - m), l = sum p;
 //  * o = sum_p p_p v_p: lane = dimension pair, V rows coalesced (256 B per
-//    position), p_p taken by readlane.
-// Partial record per head: m, l, o[128].
+//    position), p_p taken by readlane;
+//  * the 8 wave records merge in LDS into the chunk's record (m, l, o[128]) per
+//    head: M = max m_w, l = sum e^{m_w - M} l_w, o = sum e^{m_w - M} o_w.
 template <int GROUP>
-__global__ __launch_bounds__(64) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
-                                                          const std::uint32_t* __restrict__ pos_ptr,
-                                                          std::uint32_t nchunks, float* __restrict__ partials) {
-  const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
+                                                                       const std::uint32_t* __restrict__ pos_ptr,
+                                                                       std::uint32_t nchunks,
+                                                                       float* __restrict__ partials) {
+  __shared__ float qs[GROUP][4][kQPad];
+  __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
+  const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
+  const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
   const std::uint32_t p0 = c * kAttnChunk;
   float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * GROUP * (kHeadDim + 2u);
-  if (p0 > pos) {  // chunk beyond the context: empty record
-    for (std::uint32_t i = lane; i < GROUP * (kHeadDim + 2u); i += 64u)
+  if (p0 > pos) {  // chunk beyond the context (uniform over the workgroup): empty record
+    for (std::uint32_t i = threadIdx.x; i < GROUP * (kHeadDim + 2u); i += blockDim.x)
       rec[i] = (i % (kHeadDim + 2u)) == 0u ? -INFINITY : 0.0f;
     return;
   }
-  const std::uint32_t npos = (pos - p0 + 1u) < kAttnChunk ? (pos - p0 + 1u) : kAttnChunk;
-  const bool valid = lane < npos;
-  const float* qg = q + static_cast<std::size_t>(g) * GROUP * kHeadDim;
-  const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
-
-  // This lane's position (clamped into the chunk's valid range, so every
-  // address is inside the cache) and its K / V row offset (elements; the host
-  // checks that a layer's cache has fewer than 2^32 of them).
-  const std::uint32_t row_off = static_cast<std::uint32_t>(kv_offset(kv, p0 + (valid ? lane : 0u), g));
-  uint4 pk[16];
+  const std::uint32_t wp0 = p0 + kAttnSub * wave;
+  const std::uint32_t npos = wp0 > pos ? 0u : ((pos - wp0 + 1u) < kAttnSub ? (pos - wp0 + 1u) : kAttnSub);
+  const std::uint32_t pl = lane >> 2, qd = lane & 3u;
+  const bool valid = pl < npos;
+  // This lane's position (clamped to one inside the context, so every address
+  // is inside the cache) and its K / V row offset (elements; the host checks
+  // that a layer's cache has fewer than 2^32 of them).
+  const std::uint32_t row_off =
+      static_cast<std::uint32_t>(kv_offset(kv, valid ? wp0 + pl : (npos > 0u ? wp0 : p0), g));
+  uint4 pk[4];
   {
-    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off);
+    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off + (kHeadDim / 4u) * qd);
 #pragma unroll
-    for (int w = 0; w < 16; ++w) pk[w] = kr[w];
+    for (int w = 0; w < 4; ++w) pk[w] = kr[w];
   }
-  std::uint32_t vw[kAttnChunk];
+  std::uint32_t vw[kAttnSub];
 #pragma unroll
-  for (int j = 0; j < static_cast<int>(kAttnChunk); ++j) {
-    const std::uint32_t off = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_off), j));
+  for (int j = 0; j < static_cast<int>(kAttnSub); ++j) {
+    const std::uint32_t off = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_off), 4 * j));
     vw[j] = *reinterpret_cast<const std::uint32_t*>(kv.v + off + 2u * lane);
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
+  const float* qg = q + static_cast<std::size_t>(g) * GROUP * kHeadDim;
+  for (std::uint32_t i = threadIdx.x; i < GROUP * kHeadDim; i += blockDim.x) {
+    const std::uint32_t h = i / kHeadDim, d = i % kHeadDim;
+    qs[h][d / (kHeadDim / 4u)][d % (kHeadDim / 4u)] = qg[i];
+  }
+  __syncthreads();
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
   float s[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) s[h] = 0.0f;
 #pragma unroll
-  for (int w = 0; w < 16; ++w) {
+  for (int w = 0; w < 4; ++w) {
     const std::uint32_t words[4] = {pk[w].x, pk[w].y, pk[w].z, pk[w].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
       const int d = 8 * w + 2 * e;
 #pragma unroll
-      for (int h = 0; h < GROUP; ++h) s[h] += qg[h * kHeadDim + d] * k0 + qg[h * kHeadDim + d + 1] * k1;
+      for (int h = 0; h < GROUP; ++h) s[h] += qs[h][qd][d] * k0 + qs[h][qd][d + 1] * k1;
     }
   }
   float pw[GROUP], mh[GROUP], lh[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) {
-    const float sc = valid ? s[h] * scale : -INFINITY;
-    mh[h] = wave_max(sc);
-    pw[h] = valid ? expf(sc - mh[h]) : 0.0f;  // 0 for positions beyond the context
-    lh[h] = wave_sum(pw[h]);
+    float sh = s[h] + __shfl_xor(s[h], 1, 64);
+    sh += __shfl_xor(sh, 2, 64);
+    const float sc = valid ? sh * scale : -INFINITY;
+    mh[h] = wave_max(sc);  // -inf for a wave without positions
+    pw[h] = valid ? expf(sc - mh[h]) : 0.0f;
+    lh[h] = wave_sum(qd == 0u ? pw[h] : 0.0f);
   }
-  // o = sum_i p_i v_i over the chunk's 64 positions (weights of invalid ones are
-  // 0 and their rows clamped in range).
   float o0[GROUP], o1[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < static_cast<int>(kAttnChunk); ++j) {
+  for (int j = 0; j < static_cast<int>(kAttnSub); ++j) {
     const float v0 = h2f(vw[j]), v1 = h2f(vw[j] >> 16);
 #pragma unroll
     for (int h = 0; h < GROUP; ++h) {
-      const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), j));
+      const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), 4 * j));
       o0[h] += p * v0;
       o1[h] += p * v1;
     }
   }
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) {
-    float* r = rec + h * (kHeadDim + 2u);
-    *reinterpret_cast<float2*>(r + 2u + 2u * lane) = make_float2(o0[h], o1[h]);
+    *reinterpret_cast<float2*>(&wrec[wave][h][2u + 2u * lane]) = make_float2(o0[h], o1[h]);
     if (lane == 0u) {
-      r[0] = mh[h];
-      r[1] = lh[h];
+      wrec[wave][h][0] = mh[h];
+      wrec[wave][h][1] = lh[h];
+    }
+  }
+  __syncthreads();
+  if (wave != 0u) return;
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) {
+    float M = wrec[0][h][0];  // finite: wave 0 holds position p0
+#pragma unroll
+    for (std::uint32_t w = 1; w < kAttnWaves; ++w) M = fmaxf(M, wrec[w][h][0]);
+    float L = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (std::uint32_t w = 0; w < kAttnWaves; ++w) {
+      const float f = expf(wrec[w][h][0] - M);  // 0 for a wave without positions
+      const float2 o = *reinterpret_cast<const float2*>(&wrec[w][h][2u + 2u * lane]);
+      L += f * wrec[w][h][1];
+      a0 += f * o.x;
+      a1 += f * o.y;
+    }
+    float* r = rec + h * (kHeadDim + 2u);
+    *reinterpret_cast<float2*>(r + 2u + 2u * lane) = make_float2(a0, a1);
+    if (lane == 0u) {
+      r[0] = M;
+      r[1] = L;
     }
   }
 }
 
+constexpr std::uint32_t kCombinePass = 32;  // chunk records per combine pass
+
 // One wave per query head: merge the chunk records (m_c, l_c, o_c) of its kv
-// head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c. Per pass of 64
+// head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c. Per pass of 32
 // chunks every load is issued up front: lane c reads chunk c's (m, l) (wave max
-// / sum) and, as lane = dimension pair, the pass's 64 o_c rows; the weights are
+// / sum) and, as lane = dimension pair, the pass's 32 o_c rows; the weights are
 // taken by readlane. Running sums are rescaled when a later pass raises the
 // maximum.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
@@ -383,13 +422,13 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const std::size_t stride = static_cast<std::size_t>(group) * (kHeadDim + 2u);
   const float* base = partials + static_cast<std::size_t>(g) * nchunks * stride + hh * (kHeadDim + 2u);
   float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (std::uint32_t c0 = 0; c0 < n; c0 += 64u) {
-    const std::uint32_t cnt = n - c0 < 64u ? n - c0 : 64u;
-    const std::uint32_t c = c0 + (lane < cnt ? lane : cnt - 1u);
+  for (std::uint32_t c0 = 0; c0 < n; c0 += kCombinePass) {
+    const std::uint32_t cnt = n - c0 < kCombinePass ? n - c0 : kCombinePass;
+    const std::uint32_t c = c0 + (lane < cnt ? lane : cnt - 1u);  // lanes >= cnt: masked below
     const float m_raw = base[c * stride], l_raw = base[c * stride + 1u];
-    float2 ov[64];
+    float2 ov[kCombinePass];
 #pragma unroll
-    for (std::uint32_t j = 0; j < 64u; ++j) {
+    for (std::uint32_t j = 0; j < kCombinePass; ++j) {
       const std::uint32_t cj = c0 + (j < cnt ? j : cnt - 1u);
       ov[j] = *reinterpret_cast<const float2*>(base + cj * stride + 2u + 2u * lane);
     }
@@ -403,7 +442,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     L += wave_sum(ok ? w * l_raw : 0.0f);
     M = Mn;
 #pragma unroll
-    for (std::uint32_t j = 0; j < 64u; ++j) {
+    for (std::uint32_t j = 0; j < kCombinePass; ++j) {
       const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), static_cast<int>(j)));
       o0 += wj * ov[j].x;  // wj = 0 for j >= cnt
       o1 += wj * ov[j].y;
@@ -451,7 +490,16 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
                                                               std::uint32_t* pos, std::uint32_t advance) {
   __shared__ unsigned long long part[4];
   unsigned long long best = 0ull;
-  for (std::uint32_t i = threadIdx.x; i < count; i += 256u) best = keys[i] > best ? keys[i] : best;
+  for (std::uint32_t i0 = threadIdx.x; i0 < count; i0 += 256u * 8u) {
+    unsigned long long k[8];
+#pragma unroll
+    for (std::uint32_t j = 0; j < 8u; ++j) {
+      const std::uint32_t i = i0 + 256u * j;
+      k[j] = i < count ? keys[i] : 0ull;
+    }
+#pragma unroll
+    for (std::uint32_t j = 0; j < 8u; ++j) best = k[j] > best ? k[j] : best;
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const unsigned long long other = __shfl_xor(best, o, 64);
@@ -521,7 +569,7 @@ hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_h
   if (static_cast<std::uint64_t>(kv.capacity) * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const std::uint32_t group = n_heads / kv.n_kv;
   const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
-  const dim3 grid(nchunks, kv.n_kv), block(64);
+  const dim3 grid(nchunks, kv.n_kv), block(64 * kAttnWaves);
   switch (group) {
     case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
     case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
