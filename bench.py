@@ -40,6 +40,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec-set", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run a 256 MiB device copy and each decode stage of layer 0 a few times (for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), print nothing else")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
+                         "HBM bytes per launch, calibrated on the copy kernel")
     return ap.parse_args()
 
 
@@ -187,6 +193,82 @@ def decode_bench(torch, args) -> dict:
     }
 
 
+# ---- HBM traffic from counters ------------------------------------------------------
+
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = REPO / "profiles" / "decode_8b_hbm_traffic.txt"
+STAGE_KERNELS = {  # decode stage -> substring of its kernel's name
+    "qkv": "EpiQkv", "attention": "attn_partial_kernel", "o": "mv_kernel<7, 1, 4, false, rtxllm::(anonymous "
+    "namespace)::EpiResidual", "gate_up": "EpiGateUp", "down": "mv_kernel<4, 1, 4, true", "lm_head": "EpiLogits",
+}
+
+
+def traffic_probe(torch) -> None:
+    """The workload of the two counter passes: a plain fill and a plain sum of
+    COPY_BYTES (the calibration: kernels whose HBM bytes are known) and each
+    decode stage of layer 0, three times each."""
+    from rtxllm_amd.llama import LLAMA_8B
+
+    m, token = build_model(torch, LLAMA_8B)
+    m.set_token_pos(token, LLAMA_8B.max_ctx - 64)
+    buf = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    for _ in range(3):
+        buf.fill_(1.0)         # writes COPY_BYTES
+        float(buf.sum())       # reads COPY_BYTES
+        for st in ("qkv", "attention", "o", "gate_up", "down", "lm_head"):
+            m.launch_stage(0, st, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    m.close()
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> str:
+    """Per-kernel mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
+    true bytes / counter bytes of a calibration kernel: the sum (reads
+    COPY_BYTES) for FETCH_SIZE, the fill (writes COPY_BYTES) for WRITE_SIZE."""
+    import csv
+    import glob
+
+    def read(d: str, counter: str) -> dict:
+        vals: dict = {}
+        for f in glob.glob(str(Path(d) / "**" / "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in vals.items()}
+
+    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    fk = [k for k in fetch if "reduce_kernel" in k]
+    wk = [k for k in write if "FillFunctor" in k]
+    if not fk or not wk:
+        raise SystemExit("calibration kernels (sum, fill) missing from the counter runs")
+    fk, wk = max(fk, key=lambda k: fetch[k]), max(wk, key=lambda k: write[k])
+    f_scale = COPY_BYTES / (fetch[fk] * 1024.0)
+    w_scale = COPY_BYTES / (write[wk] * 1024.0)
+    lines = [f"calibration_read {COPY_BYTES} bytes: FETCH_SIZE {fetch[fk]:.0f} KiB -> fetch_scale {f_scale:.4f}",
+             f"calibration_write {COPY_BYTES} bytes: WRITE_SIZE {write[wk]:.0f} KiB -> write_scale {w_scale:.4f}"]
+    for st, key in STAGE_KERNELS.items():
+        ks = [k for k in fetch if key in k]
+        if not ks:
+            continue
+        k = ks[0]
+        fb = fetch[k] * 1024.0 * f_scale
+        wb = write.get(k, 0.0) * 1024.0 * w_scale
+        lines.append(f"{st} fetch_bytes {fb:.0f} write_bytes {wb:.0f} traffic_bytes {fb + wb:.0f}")
+    return "\n".join(lines) + "\n"
+
+
+def traffic_of(stage: str):
+    """HBM bytes per launch of a stage from the committed counter summary, or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            parts = line.split()
+            if parts and parts[0] == stage and "traffic_bytes" in parts:
+                return int(parts[parts.index("traffic_bytes") + 1])
+    except OSError:
+        pass
+    return None
+
+
 # ---- matvec set -----------------------------------------------------------------
 
 def matvec_set_bench(torch) -> dict:
@@ -286,9 +368,15 @@ def main() -> int:
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 (multi-GPU is design-only)"}))
         return 2
+    if args.traffic_summary:
+        sys.stdout.write(traffic_summary(*args.traffic_summary))
+        return 0
     import torch
 
     torch.cuda.set_device(0)
+    if args.traffic_probe:
+        traffic_probe(torch)
+        return 0
     dec = decode_bench(torch, args)
     dom = dec["stages"][dec["dominant"]]
     out = {
@@ -313,7 +401,8 @@ def main() -> int:
         "step_algorithmic_bytes": int(dec["step_bytes"]),
         "stages": dec["stages"],
         "roofline": {"bound": "hbm", "kernel": dec["dominant"], "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": dom["frac"], "traffic": None},
+                     "unit": "GB/s", "frac": dom["frac"], "traffic": traffic_of(dec["dominant"]),
+                     "algorithmic_bytes": dom["bytes"], "us_per_launch": dom["us"]},
     }
     if not args.no_matvec_set:
         out["matvec_set"] = matvec_set_bench(torch)
