@@ -74,14 +74,15 @@ class HostModel:
             self.lm_meta = None
         self.out_norm = m.download("out_norm", np.float32)
 
-    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True):
-        """Layers in place on h (float32); returns (h, logits or None)."""
+    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True, layers=None):
+        """Layers (all of this model's, or the given subset) in place on h
+        (float32); returns (h, logits or None)."""
         s, f, P = self.m.shape, self.m.formats, orc.ptr
         lib = orc.lib()
         inv_freq = np.empty(HEAD_DIM // 2, np.float32)
         lib.orc_rope_inv_freq(HEAD_DIM, s.rope_theta, P(inv_freq))
         shape = orc.LayerShape(s.hidden, s.n_heads, s.n_kv_heads, HEAD_DIM, s.ffn, s.rms_eps, P(inv_freq))
-        for l in self.layers:
+        for l in (self.layers if layers is None else layers):
             d = self.L[l]
             w = orc.LayerWeights(
                 f["fmt_qkv"], f["fmt_qkv"], f["fmt_qkv"], f["fmt_o"], f["fmt_gate_up"], f["fmt_gate_up"],

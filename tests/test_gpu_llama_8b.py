@@ -1,0 +1,111 @@
+"""GPU parity of the decode runner at the full Llama-8B shapes (hidden 4096,
+32/8 heads x 128, ffn 14336, vocab 128256, 32 layers, 4096-position paged fp16
+KV; q/k/v/o IQ3_S, gate/up IQ2_S, down Q4_K split-native, Q5_K embedding and
+LM head), against the oracle, stage by stage:
+
+* one layer at 2048 and at 4095 positions of context (the single-layer slice);
+* every one of the 32 layers of a decode step, each from the hidden state the
+  GPU produced for it, and the LM head + greedy token from the GPU's final
+  hidden state (the 32-layer step).
+
+Why per layer: with random-init weights the 32-layer network is chaotic. A
+1e-6 relative perturbation of the oracle's own input grows to ~6e-3 after four
+layers, so no implementation that is not bit-identical to the oracle can match
+its 32-layer logits to 1e-3; the per-stage comparison bounds this build's own
+error (~1e-5 per layer) instead. All calls go through the C-ABI."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from rtxllm_amd import packs  # noqa: E402
+from rtxllm_amd.llama import EMBED, HEAD, LLAMA_8B, Llama  # noqa: E402
+
+from llama_ref import HostModel  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+SEED = 0x5EED0003
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def rel(a, b) -> float:
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.fixture(scope="module")
+def model8b():
+    s = LLAMA_8B
+    m = Llama(s)
+    m.synth_weights(SEED)
+    torch.cuda.synchronize()
+    H = s.hidden
+    for l in range(s.n_layers):
+        m.upload("attn_norm", packs.normal_f32(SEED + 100 + 2 * l, H, mean=1.0, std=0.02), layer=l)
+        m.upload("ffn_norm", packs.normal_f32(SEED + 101 + 2 * l, H, mean=1.0, std=0.02), layer=l)
+        n = m.region_bytes("k_cache", l) // 2
+        m.upload("k_cache", packs.normal_f16_bits(SEED + 300 + 2 * l, n, threads=THREADS), layer=l)
+        m.upload("v_cache", packs.normal_f16_bits(SEED + 301 + 2 * l, n, threads=THREADS), layer=l)
+    m.upload("out_norm", packs.normal_f32(SEED + 99, H, mean=1.0, std=0.02))
+    yield m
+    m.close()
+
+
+def embed(m: Llama, token: int, pos: int) -> np.ndarray:
+    m.set_token_pos(token, pos)
+    m.forward(0, 0, EMBED)  # embedding gather only
+    torch.cuda.synchronize()
+    return m.download("h", np.float32)
+
+
+@pytest.mark.parametrize("pos", [2047, 4094])
+def test_8b_layer_slice_matches_oracle(orc, model8b, pos):
+    m = model8b
+    ref = HostModel(m, range(1))
+    token = 40960 + pos
+    h0 = embed(m, token, pos)
+    assert rel(h0, ref.embed_row(orc, token)) == 0.0  # the Q5_K gather is bit-exact
+    m.forward(0, 1, 0)
+    torch.cuda.synchronize()
+    h_gpu = m.download("h", np.float32)
+    h_ref, _ = ref.run(orc, h0.copy(), pos, threads=THREADS, head=False)
+    assert np.all(np.isfinite(h_gpu))
+    assert rel(h_gpu, h_ref) <= TOL
+
+
+def test_8b_decode_step_each_stage_matches_oracle(orc, model8b):
+    m, s = model8b, LLAMA_8B
+    ref = HostModel(m, range(s.n_layers))
+    pos, token = s.max_ctx - 2, 1234
+    h = embed(m, token, pos)
+    worst = 0.0
+    for l in range(s.n_layers):
+        m.forward(l, l + 1, 0)  # re-stages h with layer l's attention norm, then layer l
+        torch.cuda.synchronize()
+        h_gpu = m.download("h", np.float32)
+        h_ref, _ = ref.run(orc, h.copy(), pos, threads=THREADS, head=False, layers=[l])
+        assert np.all(np.isfinite(h_gpu)), l
+        err = rel(h_gpu, h_ref)
+        assert err <= TOL, (l, err)
+        worst = max(worst, err)
+        h = h_gpu
+    # LM head and greedy token from the GPU's final hidden state
+    m.forward(s.n_layers, s.n_layers, HEAD)
+    torch.cuda.synchronize()
+    logits = m.download("logits", np.float32)
+    _, logits_ref = ref.run(orc, h.copy(), pos, threads=THREADS, head=True, layers=[])
+    assert rel(logits, logits_ref) <= TOL
+    tok = int(m.download("token", np.uint32)[0])
+    assert tok == int(np.argmax(logits))
+    top2 = np.sort(logits_ref)[-2:]
+    if top2[1] - top2[0] > 1e-3 * abs(top2[1]):
+        assert tok == int(np.argmax(logits_ref))
+    assert int(m.download("pos", np.uint32)[0]) == pos + 1
+    print(f"worst per-layer relative error {worst:.2e}")
