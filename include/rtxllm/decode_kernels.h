@@ -10,9 +10,11 @@
  *
  * The rtxllm_* entry points without "launch" in their names have no
  * counterpart in the reference; they carry the math of a real Llama decode step
- * (pure y = W x, weighted RMSNorm, RoPE with a theta schedule, SiLU-gate
- * multiply, Q5_K embedding gather, GQA attention over a paged fp16 KV cache,
- * greedy argmax, batch-8 skinny GEMM) and the host-side pack helpers.
+ * (pure y = W x on an fp32 or a staged activation) and the host-side pack
+ * helpers; the Llama layer math (weighted RMSNorm, RoPE with a theta schedule,
+ * SiLU-gate multiply, Q5_K embedding gather, GQA attention over a paged fp16
+ * KV cache, greedy argmax) is reached through the decode runner of
+ * rtxllm/llama.h.
  *
  * Pack layouts (all row-major, rows x (cols / 256) blocks, cols % 256 == 0):
  *   Q4_K raw 144 B, Q5_K 176 B, IQ2_S 82 B, IQ3_S 110 B GGUF blocks;
@@ -199,13 +201,14 @@ hipError_t rtxllm_matvec(int format, const uint8_t* payload, const uint8_t* meta
                          uint32_t rows, uint32_t cols, hipStream_t stream);
 
 /* Staged activation ("xq"): x is cut into 16-value groups; each group is kept as
- * 15-bit fixed point X_j = rint(x_j * 16256 / max|x|) split into int8 digits
- * X_j = 128 H_j + L_j, plus the group scale s = max|x| / 16256 and the group
- * sum s * sum(X). Layout of one buffer of rtxllm_xq_bytes(cols) bytes: H[cols],
- * L[cols] (int8), s[cols/16], sum[cols/16] (f32). The matvec kernels multiply
- * the weight codes with the digits through exact integer dot products, so the
- * staging rounding (relative step 6.2e-5 of the group maximum) is the only
- * deviation from an fp32 product. */
+ * 22-bit fixed point X_j = rint(x_j * K / max|x|), K = 127 * 16384 = 2080768,
+ * split into three int8 digits X_j = 16384 H_j + 128 M_j + L_j (H in
+ * [-127, 127], M in [-64, 64], L in [-64, 63]), plus the group scale
+ * s = max|x| / K and the group sum s * sum(X). Layout of one buffer of
+ * rtxllm_xq_bytes(cols) bytes: H[cols], M[cols], L[cols] (int8), s[cols/16],
+ * sum[cols/16] (f32). The matvec kernels multiply the weight codes with the
+ * digits through exact integer dot products, so the staging rounding (relative
+ * step 4.8e-7 of the group maximum) is the only deviation from an fp32 product. */
 size_t rtxllm_xq_bytes(uint32_t cols);
 /* xq = stage(x * weight) (weight may be null: stage x). cols % 256 == 0. */
 hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t cols, void* xq,

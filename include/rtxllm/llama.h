@@ -52,7 +52,9 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * (meta regions exist for Q4_K split layouts only), "attn_norm", "ffn_norm",
  * "k_cache", "v_cache" (fp16 [pages][n_kv][page_size][128]), "block_table"
  * (int32 [max_ctx / page_size]). Global (layer ignored): "embed", "lm_head",
- * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos".
+ * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos",
+ * and the work buffers "xq" / "xq_att" (staged activations), "sumsq",
+ * "attn_partials", "argkeys", "inv_freq".
  * Row layouts: qkv = q rows (n_heads*128) | k rows | v rows; gate_up rows
  * interleaved (2i = gate_i, 2i+1 = up_i). */
 void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes);
