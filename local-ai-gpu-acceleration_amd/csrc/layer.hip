@@ -606,7 +606,7 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
 
 std::uint32_t logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols) {
   MvGeom g;
-  if (!mv_geom(fmt, rows, cols, EpiLogits::kTile, 0u, g)) return 0u;
+  if (!mv_geometry<false, EpiLogits>(fmt, rows, cols, g)) return 0u;
   return g.grid * g.nrg;
 }
 

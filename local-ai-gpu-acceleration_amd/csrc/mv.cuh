@@ -335,55 +335,72 @@ __device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uin
   m1 = dmin * static_cast<float>((mn >> 8) & 0xFFu);
 }
 
+// IQ units in two phases, so the LDS lookups of one row can be in flight while
+// the previous row's dot products run: unit_lookup issues the codebook and
+// sign-table reads and applies the signs; unit_dot_iq multiplies the signed
+// int8 words with the activation digits.
+struct IqWords {
+  std::uint32_t w[8];  // signed int8 weights, 4 per word, in value order
+};
+
 template <int FMT>
-__device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u, std::uint32_t k, const XG& x0,
-                                              const XG& x1, const IqLds<FMT>* t) {
+__device__ __forceinline__ void unit_lookup(const UnitRaw& r, const IqLds<FMT>* t, IqWords& q) {
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
       const uint2 gm = t->grid2[idx];
       const uint4 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
-      const int w0 = static_cast<int>((gm.x ^ sm.x) + sm.z);
-      const int w1 = static_cast<int>((gm.y ^ sm.y) + sm.w);
-      const XG& xg = grp < 2 ? x0 : x1;
-      const int o = (grp & 1) * 2, s = grp >> 1;
-      ah[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.h[o]), ah[s], false);
-      ah[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.h[o + 1]), ah[s], false);
-      am[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.m[o]), am[s], false);
-      am[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.m[o + 1]), am[s], false);
-      al[s] = __builtin_amdgcn_sdot4(w0, static_cast<int>(xg.l[o]), al[s], false);
-      al[s] = __builtin_amdgcn_sdot4(w1, static_cast<int>(xg.l[o + 1]), al[s], false);
+      q.w[2 * grp] = (gm.x ^ sm.x) + sm.z;
+      q.w[2 * grp + 1] = (gm.y ^ sm.y) + sm.w;
     }
-    const float d = h2f(r.c[0]);
-    const float s0 = d * (0.5f + static_cast<float>(r.c[2] & 15u)) * 0.25f;
-    const float s1 = d * (0.5f + static_cast<float>(r.c[2] >> 4)) * 0.25f;
-    return (s0 * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
-           (s1 * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
-  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
+  } else {
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const uint4 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
-      const XG& xg = grp < 2 ? x0 : x1;
-      const int o = (grp & 1) * 2, s = grp >> 1;
 #pragma unroll
       for (int pair = 0; pair < 2; ++pair) {
         const int sel = 2 * grp + pair;
         const std::uint32_t qb = (r.a[sel >> 2] >> (8 * (sel & 3))) & 0xFFu;
         const std::uint32_t idx = qb | (((r.c[1] >> sel) & 1u) << 8);
-        const int w = static_cast<int>((t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z));
-        ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o + pair]), ah[s], false);
-        am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o + pair]), am[s], false);
-        al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o + pair]), al[s], false);
+        q.w[sel] = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z);
       }
     }
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, std::uint32_t k, const XG& x0, const XG& x1,
+                                             const IqWords& q) {
+  int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const XG& xg = j < 4 ? x0 : x1;
+    const int s = j >> 2, o = j & 3;
+    const int w = static_cast<int>(q.w[j]);
+    ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o]), ah[s], false);
+    am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o]), am[s], false);
+    al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
+  }
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    const float d = h2f(r.c[0]);
+    const float s0 = d * (0.5f + static_cast<float>(r.c[2] & 15u)) * 0.25f;
+    const float s1 = d * (0.5f + static_cast<float>(r.c[2] >> 4)) * 0.25f;
+    return (s0 * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
+           (s1 * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
+  } else {
     const std::uint32_t nib = (k & 1u) ? (r.c[2] >> 4) : (r.c[2] & 15u);
     const float scale = h2f(r.c[0]) * static_cast<float>(1u + 2u * nib);
     return (scale * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
            (scale * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
-  } else {
+  }
+}
+
+// K-quant unit: weight codes, scales and the dot with the staged activation.
+template <int FMT>
+__device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u, std::uint32_t k, const XG& x0,
+                                              const XG& x1) {
+  {
     const std::uint32_t g = u.g;
     std::uint32_t lo[4], hi[4];
 #pragma unroll
@@ -495,6 +512,12 @@ __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane
 // ---- the kernel -------------------------------------------------------------
 
 constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slots)
+
+// Tile buffers per row group (tiles in flight + 1).
+template <int FMT>
+constexpr int pipe_depth() {
+  return 2;
+}
 
 // Rows per epilogue group: epilogues that declare kGroupRows (a multiple of
 // their tile) receive the results of kGroupRows consecutive rows at once.
@@ -623,8 +646,12 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       xg_load(xs.xq, g1, x1[i]);
     }
   }
-  UnitRaw ra[TILE][UPL], rb[TILE][UPL];
-  load_tile(tile_of(0u), ra);
+  // A ring of NB tile buffers: tile s + NB - 1 is requested before tile s is
+  // computed, so each row group keeps NB - 1 tiles of weights in flight.
+  constexpr int NB = pipe_depth<FMT>();
+  UnitRaw buf[NB][TILE][UPL];
+#pragma unroll
+  for (int b = 0; b + 1 < NB; ++b) load_tile(tile_of(static_cast<std::uint32_t>(b)), buf[b]);
   if constexpr (fmt_is_iq(FMT)) __syncthreads();
 
   auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, std::uint32_t gpar, const UnitRaw (&raw)[TILE][UPL]) {
@@ -633,14 +660,34 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     const bool active = t < tiles;
     float acc[TILE];
 #pragma unroll
-    for (int rr = 0; rr < TILE; ++rr) {
-      acc[rr] = 0.0f;
-      if (active) {
+    for (int rr = 0; rr < TILE; ++rr) acc[rr] = 0.0f;
+    if (active) {
+      // a lane past the row's last unit computes a clamped copy and adds 0
+      if constexpr (fmt_is_iq(FMT)) {
+        // row rr + 1's codebook lookups are issued before row rr's dot products
+        IqWords q[2][UPL];
 #pragma unroll
-        for (int i = 0; i < UPL; ++i) {
-          // a lane past the row's last unit computes a clamped copy and adds 0
-          const float v = unit_compute<FMT>(raw[rr][i], off[i], uk[i], x0[i], x1[i], tables);
-          acc[rr] += uvalid[i] ? v : 0.0f;
+        for (int i = 0; i < UPL; ++i) unit_lookup<FMT>(raw[0][i], tables, q[0][i]);
+#pragma unroll
+        for (int rr = 0; rr < TILE; ++rr) {
+          if (rr + 1 < TILE) {
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) unit_lookup<FMT>(raw[rr + 1][i], tables, q[(rr + 1) & 1][i]);
+          }
+#pragma unroll
+          for (int i = 0; i < UPL; ++i) {
+            const float v = unit_dot_iq<FMT>(raw[rr][i], uk[i], x0[i], x1[i], q[rr & 1][i]);
+            acc[rr] += uvalid[i] ? v : 0.0f;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < TILE; ++rr) {
+#pragma unroll
+          for (int i = 0; i < UPL; ++i) {
+            const float v = unit_compute<FMT>(raw[rr][i], off[i], uk[i], x0[i], x1[i]);
+            acc[rr] += uvalid[i] ? v : 0.0f;
+          }
         }
       }
     }
@@ -672,14 +719,15 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     }
   };
 
-  for (std::uint32_t s = 0; s < rounds; s += 2u) {
-    load_tile(tile_of(s + 1u), rb);
-    finish_tile(tile_of(s), 0u, (s >> rshift) & 1u, ra);
-    group_end(s);
-    if (s + 1u >= rounds) break;
-    load_tile(tile_of(s + 2u), ra);
-    finish_tile(tile_of(s + 1u), 1u, ((s + 1u) >> rshift) & 1u, rb);
-    group_end(s + 1u);
+  for (std::uint32_t s = 0; s < rounds; s += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const std::uint32_t sj = s + static_cast<std::uint32_t>(j);
+      if (sj >= rounds) break;  // uniform over the workgroup
+      load_tile(tile_of(sj + NB - 1u), buf[(j + NB - 1) % NB]);
+      finish_tile(tile_of(sj), sj & 1u, (sj >> rshift) & 1u, buf[j]);
+      group_end(sj);
+    }
   }
   if constexpr (EpiHasFinish<Epi>::value) {
     if (kw == 0u) epi.finish(blockIdx.x * nrg + rg, lane);
