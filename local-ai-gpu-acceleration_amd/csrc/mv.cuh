@@ -369,30 +369,53 @@ __device__ __forceinline__ void unit_lookup(const UnitRaw& r, const IqLds<FMT>* 
   }
 }
 
+// Per-lane scale factors of an IQ unit's two 16-value halves, fixed for the
+// launch: IQ2_S sub-scale (0.5 + n) / 4 folded with the activation scale as
+// n * a + b (a = s / 4, b = s / 8); IQ3_S takes the scale nibble's shift.
+struct IqLaneScale {
+  float a0, b0, a1, b1;
+  std::uint32_t nib_shift;
+};
+
 template <int FMT>
-__device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, std::uint32_t k, const XG& x0, const XG& x1,
+__device__ __forceinline__ IqLaneScale iq_lane_scale(std::uint32_t k, const XG& x0, const XG& x1) {
+  IqLaneScale ls;
+  ls.a0 = 0.25f * x0.s, ls.b0 = 0.125f * x0.s;
+  ls.a1 = 0.25f * x1.s, ls.b1 = 0.125f * x1.s;
+  ls.nib_shift = (k & 1u) ? 4u : 0u;
+  return ls;
+}
+
+template <int FMT>
+__device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, const XG& x1, const IqLaneScale& ls,
                                              const IqWords& q) {
-  int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
+  int ah[2], am[2], al[2];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const XG& xg = j < 4 ? x0 : x1;
-    const int s = j >> 2, o = j & 3;
-    const int w = static_cast<int>(q.w[j]);
-    ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o]), ah[s], false);
-    am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o]), am[s], false);
-    al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
+  for (int s = 0; s < 2; ++s) {
+    const XG& xg = s ? x1 : x0;
+    ah[s] = sdot4_0(q.w[4 * s], xg.h[0]);
+    am[s] = sdot4_0(q.w[4 * s], xg.m[0]);
+    al[s] = sdot4_0(q.w[4 * s], xg.l[0]);
+#pragma unroll
+    for (int o = 1; o < 4; ++o) {
+      const int w = static_cast<int>(q.w[4 * s + o]);
+      ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o]), ah[s], false);
+      am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o]), am[s], false);
+      al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
+    }
   }
+  const float d = h2f(r.c[0]);
+  const float D0 = static_cast<float>(dot_digits(ah[0], am[0], al[0]));
+  const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    const float d = h2f(r.c[0]);
-    const float s0 = d * (0.5f + static_cast<float>(r.c[2] & 15u)) * 0.25f;
-    const float s1 = d * (0.5f + static_cast<float>(r.c[2] >> 4)) * 0.25f;
-    return (s0 * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
-           (s1 * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
+    // d * (0.5 + n) / 4 * s = d * (n * s / 4 + s / 8)
+    const float f0 = __builtin_fmaf(static_cast<float>(r.c[2] & 15u), ls.a0, ls.b0);
+    const float f1 = __builtin_fmaf(static_cast<float>(r.c[2] >> 4), ls.a1, ls.b1);
+    return d * __builtin_fmaf(f1, D1, f0 * D0);
   } else {
-    const std::uint32_t nib = (k & 1u) ? (r.c[2] >> 4) : (r.c[2] & 15u);
-    const float scale = h2f(r.c[0]) * static_cast<float>(1u + 2u * nib);
-    return (scale * x0.s) * static_cast<float>(dot_digits(ah[0], am[0], al[0])) +
-           (scale * x1.s) * static_cast<float>(dot_digits(ah[1], am[1], al[1]));
+    // d * (1 + 2 n) for the whole unit
+    const float m = __builtin_fmaf(static_cast<float>((r.c[2] >> ls.nib_shift) & 15u), 2.0f, 1.0f);
+    return (d * m) * __builtin_fmaf(x1.s, D1, x0.s * D0);
   }
 }
 
@@ -653,6 +676,11 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
 #pragma unroll
   for (int b = 0; b + 1 < NB; ++b) load_tile(tile_of(static_cast<std::uint32_t>(b)), buf[b]);
   if constexpr (fmt_is_iq(FMT)) __syncthreads();
+  IqLaneScale ls[UPL];
+  if constexpr (fmt_is_iq(FMT)) {
+#pragma unroll
+    for (int i = 0; i < UPL; ++i) ls[i] = iq_lane_scale<FMT>(uk[i], x0[i], x1[i]);
+  }
 
   auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, std::uint32_t gpar, const UnitRaw (&raw)[TILE][UPL]) {
     // Every wave of the workgroup runs the same rounds, so the barrier below is
@@ -676,7 +704,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
           }
 #pragma unroll
           for (int i = 0; i < UPL; ++i) {
-            const float v = unit_dot_iq<FMT>(raw[rr][i], uk[i], x0[i], x1[i], q[rr & 1][i]);
+            const float v = unit_dot_iq<FMT>(raw[rr][i], x0[i], x1[i], ls[i], q[rr & 1][i]);
             acc[rr] += uvalid[i] ? v : 0.0f;
           }
         }

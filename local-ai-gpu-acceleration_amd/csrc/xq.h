@@ -155,14 +155,26 @@ __device__ __forceinline__ void xg_store(const XQOut& x, std::uint32_t group, co
 }
 
 // sum_j w_j X_j = 16384 sum w H + 128 sum w M + sum w L, exact in int32 for
-// weights |w| <= 31 (|result| < 16 * 31 * 2^21 < 2^31).
-__device__ __forceinline__ int dot_digits(int ah, int am, int al) { return ah * 16384 + am * 128 + al; }
+// weights |w| <= 31 (|result| < 16 * 31 * 2^21 < 2^31); two shift-adds.
+__device__ __forceinline__ int dot_digits(int ah, int am, int al) {
+  const std::uint32_t lo = (static_cast<std::uint32_t>(am) << 7) + static_cast<std::uint32_t>(al);
+  return static_cast<int>((static_cast<std::uint32_t>(ah) << 14) + lo);
+}
+
+// a . b over four int8 lanes, starting a chain from 0: the three-operand
+// encoding with an inline zero accumulator (the two-operand accumulate form
+// would need the zero moved into its destination first).
+__device__ __forceinline__ int sdot4_0(std::uint32_t a, std::uint32_t b) {
+  int r;
+  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 
 // The dot of 16 int8 weights (4 words) with a staged group.
 __device__ __forceinline__ int dot16(const std::uint32_t w[4], const XG& x) {
-  int ah = 0, am = 0, al = 0;
+  int ah = sdot4_0(w[0], x.h[0]), am = sdot4_0(w[0], x.m[0]), al = sdot4_0(w[0], x.l[0]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 1; i < 4; ++i) {
     ah = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.h[i]), ah, false);
     am = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.m[i]), am, false);
     al = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.l[i]), al, false);
