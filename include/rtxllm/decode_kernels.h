@@ -217,6 +217,24 @@ hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t
 hipError_t rtxllm_matvec_xq(int format, const uint8_t* payload, const uint8_t* meta, const void* xq, float* y,
                             uint32_t rows, uint32_t cols, hipStream_t stream);
 
+/* Batched matvec on the matrix cores: y[s][rows] = W x_s for s < batch <= 8
+ * (the batch-8 decode variant). Formats: 0 Q4_K raw, 4 Q4_K split-native,
+ * 5 Q5_K, 6 IQ2_S, 7 IQ3_S; cols % 512 == 0.
+ * Staged batch activation ("x16"), rtxllm_x16_bytes(cols) bytes: 16 fp16
+ * columns of cols values, column 2 s = hi, 2 s + 1 = lo of x_s 2^-e_s (hi =
+ * fp16(x'), lo = fp16(x' - hi), e_s the power of two putting max |x'| in
+ * [0.5, 1)), then int32 e[8]. The weight codes times their sub-block scale
+ * integers are exact in fp16, so each product is exact and only the ~22-bit
+ * hi/lo split and the fp32 accumulation round. Matrices wider than 4096
+ * columns need a workspace of rtxllm_matvec_batch_workspace() bytes (0: none). */
+size_t rtxllm_x16_bytes(uint32_t cols);
+hipError_t rtxllm_stage_batch(const float* x /* [batch][cols] */, uint32_t batch, uint32_t cols, void* x16,
+                              hipStream_t stream);
+size_t rtxllm_matvec_batch_workspace(int format, uint32_t rows, uint32_t cols);
+hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
+                               float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
+                               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Host-side helpers (no device work). */
 uint32_t rtxllm_format_payload_block_bytes(int format);
 uint32_t rtxllm_format_meta_block_bytes(int format);

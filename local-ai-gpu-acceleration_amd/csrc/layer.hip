@@ -297,23 +297,33 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
   __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
   const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
   const std::uint32_t p0 = c * kAttnChunk;
+  const std::uint32_t wp0 = p0 + kAttnSub * wave;
+  const std::uint32_t pl = lane >> 2, qd = lane & 3u;
+  // The lane's position and the chunk's first position, clamped into the
+  // cache, and their block-table entries are read together with *pos: none of
+  // these loads waits for another.
+  const std::uint32_t pc = p0 < kv.capacity ? p0 : kv.capacity - 1u;
+  const std::uint32_t pl_pos = wp0 + pl < kv.capacity ? wp0 + pl : kv.capacity - 1u;
+  const std::uint32_t page_c = static_cast<std::uint32_t>(kv.block_table[pc / kv.page_size]);
+  const std::uint32_t page_w = static_cast<std::uint32_t>(kv.block_table[pl_pos / kv.page_size]);
+  const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
   float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * GROUP * (kHeadDim + 2u);
   if (p0 > pos) {  // chunk beyond the context (uniform over the workgroup): empty record
     for (std::uint32_t i = threadIdx.x; i < GROUP * (kHeadDim + 2u); i += blockDim.x)
       rec[i] = (i % (kHeadDim + 2u)) == 0u ? -INFINITY : 0.0f;
     return;
   }
-  const std::uint32_t wp0 = p0 + kAttnSub * wave;
   const std::uint32_t npos = wp0 > pos ? 0u : ((pos - wp0 + 1u) < kAttnSub ? (pos - wp0 + 1u) : kAttnSub);
-  const std::uint32_t pl = lane >> 2, qd = lane & 3u;
   const bool valid = pl < npos;
-  // This lane's position (clamped to one inside the context, so every address
-  // is inside the cache) and its K / V row offset (elements; the host checks
-  // that a layer's cache has fewer than 2^32 of them).
-  const std::uint32_t row_off =
-      static_cast<std::uint32_t>(kv_offset(kv, valid ? wp0 + pl : (npos > 0u ? wp0 : p0), g));
+  // K / V row offset (elements; the host checks that a layer's cache has fewer
+  // than 2^32 of them). A lane past the context reads the chunk's first row
+  // (inside the context, so finite data) and is weighted 0.
+  auto row_of = [&](std::uint32_t page, std::uint32_t p) {
+    return static_cast<std::uint32_t>(((static_cast<std::size_t>(page) * kv.n_kv + g) * kv.page_size +
+                                       p % kv.page_size) * kHeadDim);
+  };
+  const std::uint32_t row_off = valid ? row_of(page_w, pl_pos) : row_of(page_c, pc);
   uint4 pk[4];
   {
     const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off + (kHeadDim / 4u) * qd);
@@ -412,13 +422,12 @@ constexpr std::uint32_t kCombinePass = 32;  // chunk records per combine pass
 // taken by readlane. Running sums are rescaled when a later pass raises the
 // maximum.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
-                                                          const std::uint32_t* pos_ptr, std::uint32_t capacity,
                                                           std::uint32_t nchunks, float* __restrict__ att, XQOut xq) {
   const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
   const std::uint32_t g = head / group, hh = head % group;
-  const std::uint32_t pos = *pos_ptr < capacity ? *pos_ptr : capacity - 1u;
-  const std::uint32_t active = pos / kAttnChunk + 1u;
-  const std::uint32_t n = active < nchunks ? active : nchunks;
+  // every chunk record is merged: chunks past the context hold (-inf, 0, 0),
+  // so the kernel needs no position and starts loading at once
+  const std::uint32_t n = nchunks;
   const std::size_t stride = static_cast<std::size_t>(group) * (kHeadDim + 2u);
   const float* base = partials + static_cast<std::size_t>(g) * nchunks * stride + hh * (kHeadDim + 2u);
   float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
@@ -580,8 +589,8 @@ hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_h
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
   if (xq_att == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, partials, group, pos, kv.capacity,
-                     nchunks, att, xq_out(xq_att, n_heads * kHeadDim));
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, partials, group, nchunks, att,
+                     xq_out(xq_att, n_heads * kHeadDim));
   return hipGetLastError();
 }
 

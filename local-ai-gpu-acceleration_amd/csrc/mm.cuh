@@ -1,0 +1,394 @@
+// Batched (up to 8 activation vectors) dequant-matvec on the matrix cores:
+// Y[s][r] = sum_c W[r][c] X[s][c] for s < batch, W in a GGUF pack.
+//
+// Operands of v_mfma_f32_16x16x32_f16 (lane layouts checked on gfx950):
+//   A (16 rows x 32 k):  lane l holds A[l % 16][8 (l / 16) + i], i < 8;
+//   B (32 k x 16 cols):  lane l holds B[8 (l / 16) + i][l % 16];
+//   C (16 x 16, fp32):   lane l holds C[4 (l / 16) + i][l % 16], i < 4.
+// The k order inside one instruction is free as long as A and B agree. Lane
+// q = l / 16 of a 256-value block takes values [64 q, 64 q + 64), eight per
+// instruction (instruction j: values 64 q + 8 j .. + 8), so each lane reads its
+// weight fields as a few contiguous runs.
+//
+// * A: the weight codes times their sub-block scale integer, in fp16. These
+//   products are small integers (IQ2_S |mag (2n+1)| <= 217, IQ3_S <= 465, Q4_K
+//   q sc <= 945, Q5_K <= 1953), exact in fp16. K-quant mins go through a second
+//   product with A = the sub-block's m (<= 63).
+// * B: column n = 2 s + h holds sequence s's activation as two fp16 halves
+//   (h = 0: hi = fp16(x'), h = 1: lo = fp16(x' - hi)), x' = x 2^-e_s with a
+//   per-sequence power of two that puts max |x'| in [0.5, 1): ~22 bits of x.
+// * C accumulates one 256-value block exactly-rounded in fp32 (every A*B
+//   product is exact); per block the rows' fp16 super-block scale d (and dmin)
+//   multiply it into the fp32 result.
+//
+// A wave owns a panel of 512 columns (two blocks) for the whole launch, its 16
+// B operands (64 VGPRs) loaded once; a workgroup holds up to 8 panels (one wave
+// each) and loops over 16-row tiles, combining the panels' partial sums in LDS.
+// Matrices wider than 8 panels split into panel groups whose partial results a
+// second kernel adds.
+#pragma once
+
+#include <type_traits>
+
+#include "mv.cuh"
+
+namespace rtxllm {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr std::uint32_t kBatchMax = 8;
+constexpr std::uint32_t kPanel = 512;        // columns per wave
+constexpr std::uint32_t kMaxPanels = 8;      // waves per workgroup
+
+// Staged batch activation: x16[n][cols] fp16 (n = 2 s + h, 16 columns), then
+// int32 e[8].
+__host__ __device__ inline std::size_t x16_bytes(std::uint32_t cols) {
+  return 32u * static_cast<std::size_t>(cols) + 4u * kBatchMax;
+}
+
+constexpr bool fmt_mm_supported(int f) {
+  return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S || f == RTXLLM_FMT_Q5K || f == RTXLLM_FMT_Q4K_RAW ||
+         f == RTXLLM_FMT_Q4K_SPLIT_NATIVE;
+}
+
+// ---- LDS tables: fp16 codebooks and fp16 sign masks ------------------------------
+
+// grid2h: IQ2_S entry -> 8 fp16 magnitudes 2 l + 1; grid3h: IQ3_S entry -> 4
+// fp16 magnitudes; sign16: sign byte -> 8 x 0x8000 / 0 masks.
+struct MmLds2 {
+  uint4 grid2h[1024];
+  uint4 sign16[256];
+};
+struct MmLds3 {
+  uint2 grid3h[512];
+  uint4 sign16[256];
+};
+template <int FMT>
+using MmLds = typename std::conditional<FMT == RTXLLM_FMT_IQ2S, MmLds2, MmLds3>::type;
+
+constexpr std::uint16_t f16_of_small(std::uint32_t v) {  // exact fp16 bits of an integer 1..2047
+  std::uint32_t e = 0;
+  while ((v >> (e + 1)) != 0u) ++e;
+  const std::uint32_t mant = (v << (10 - e)) & 0x3FFu;
+  return static_cast<std::uint16_t>(((e + 15u) << 10) | mant);
+}
+
+template <std::size_t N>
+constexpr void mm_image_signs(IqImage<N>& im, std::size_t at) {
+  for (std::uint32_t i = 0; i < 256u; ++i)
+    for (std::uint32_t j = 0; j < 4u; ++j) {
+      const std::uint32_t lo = ((i >> (2 * j)) & 1u) ? 0x8000u : 0u;
+      const std::uint32_t hi = ((i >> (2 * j + 1)) & 1u) ? 0x8000u : 0u;
+      im.w[at + 4 * i + j] = lo | (hi << 16);
+    }
+}
+constexpr IqImage<5120> mm2_image() {
+  IqImage<5120> im{};
+  for (std::uint32_t i = 0; i < 1024u; ++i)
+    for (std::uint32_t j = 0; j < 4u; ++j) {
+      const std::uint32_t w = kIq2sGridSrc[i];
+      const std::uint32_t lo = f16_of_small(2u * ((w >> (4 * j)) & 3u) + 1u);
+      const std::uint32_t hi = f16_of_small(2u * ((w >> (4 * j + 2)) & 3u) + 1u);
+      im.w[4 * i + j] = lo | (hi << 16);
+    }
+  mm_image_signs(im, 4096);
+  return im;
+}
+constexpr IqImage<2048> mm3_image() {
+  IqImage<2048> im{};
+  for (std::uint32_t i = 0; i < 512u; ++i)
+    for (std::uint32_t j = 0; j < 2u; ++j) {
+      const std::uint32_t w = kIq3sGridSrc[i];
+      const std::uint32_t lo = f16_of_small((w >> (16 * j)) & 0xFFu);
+      const std::uint32_t hi = f16_of_small((w >> (16 * j + 8)) & 0xFFu);
+      im.w[2 * i + j] = lo | (hi << 16);
+    }
+  mm_image_signs(im, 1024);
+  return im;
+}
+static_assert(sizeof(IqImage<5120>) == sizeof(MmLds2) && sizeof(IqImage<2048>) == sizeof(MmLds3), "mm images");
+__device__ const IqImage<5120> kMm2Image = mm2_image();
+__device__ const IqImage<2048> kMm3Image = mm3_image();
+
+template <int FMT>
+__device__ __forceinline__ MmLds<FMT>& mm_lds() {
+  __shared__ MmLds<FMT> t;
+  return t;
+}
+
+template <int FMT>
+__device__ __forceinline__ void mm_lds_fetch(MmLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
+  constexpr std::uint32_t kChunks = sizeof(MmLds<FMT>) / 1024u;
+  static_assert(sizeof(MmLds<FMT>) % 1024u == 0u, "whole wave chunks");
+  const std::uint32_t nw = blockDim.x >> 6;
+  const uint4* src = reinterpret_cast<const uint4*>(FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kMm2Image)
+                                                                           : static_cast<const void*>(&kMm3Image));
+  uint4* dst = reinterpret_cast<uint4*>(&t);
+  for (std::uint32_t c = wave; c < kChunks; c += nw)
+    __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
+                                     (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
+}
+
+// ---- per-lane block fields --------------------------------------------------------
+
+// Lane q's fields of one 256-value block (values [64 q, 64 q + 64)).
+struct MmRaw {
+  std::uint32_t a[8];  // IQ2_S: qs[0..1] signs[2..3]; IQ3_S: qs[0..3] signs[4..5]; K: quants (32 B)
+  std::uint32_t b[8];  // Q5_K: qh (32 B)
+  std::uint32_t h[4];  // K: the 16 B head (d, dmin, scales); IQ: [0] d, [1] qh pair, [2] scale byte(s)
+};
+
+template <int FMT>
+__device__ __forceinline__ void mm_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, std::uint32_t blk,
+                                        std::uint32_t q, MmRaw& r) {
+  constexpr int P = load_policy<FMT>();
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    const std::uint32_t o = blk * 82u;
+    const u32x2 qs = bld_u64<P>(rp, o + 2u + 8u * q, sp);
+    const u32x2 sg = bld_u64<P>(rp, o + 34u + 8u * q, sp);
+    r.a[0] = qs.x, r.a[1] = qs.y, r.a[2] = sg.x, r.a[3] = sg.y;
+    r.h[0] = bld_u16<P>(rp, o, sp);
+    r.h[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
+    r.h[2] = bld_u16<P>(rp, o + 74u + 2u * q, sp);
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
+    const std::uint32_t o = blk * 110u;
+    const u32x2 q0 = bld_u64<P>(rp, o + 2u + 16u * q, sp);
+    const u32x2 q1 = bld_u64<P>(rp, o + 10u + 16u * q, sp);
+    const u32x2 sg = bld_u64<P>(rp, o + 74u + 8u * q, sp);
+    r.a[0] = q0.x, r.a[1] = q0.y, r.a[2] = q1.x, r.a[3] = q1.y, r.a[4] = sg.x, r.a[5] = sg.y;
+    r.h[0] = bld_u16<P>(rp, o, sp);
+    r.h[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
+    r.h[2] = bld_u8<P>(rp, o + 106u + q, sp);
+  } else {
+    std::uint32_t qo, ho;
+    Rsrc hr = rp;
+    std::uint32_t hs = sp;
+    if constexpr (FMT == RTXLLM_FMT_Q5K) {
+      qo = blk * 176u + 48u + 32u * q, ho = blk * 176u;
+      const u32x4 h0 = bld_u128<P>(rp, blk * 176u + 16u, sp);
+      const u32x4 h1 = bld_u128<P>(rp, blk * 176u + 32u, sp);
+      r.b[0] = h0.x, r.b[1] = h0.y, r.b[2] = h0.z, r.b[3] = h0.w;
+      r.b[4] = h1.x, r.b[5] = h1.y, r.b[6] = h1.z, r.b[7] = h1.w;
+    } else if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) {
+      qo = blk * 144u + 16u + 32u * q, ho = blk * 144u;
+    } else {  // split-native: 128 B payload, 16 B head in the metadata stream
+      qo = blk * 128u + 32u * q, ho = blk * 16u;
+      hr = rm, hs = sm;
+    }
+    const u32x4 a0 = bld_u128<P>(rp, qo, sp);
+    const u32x4 a1 = bld_u128<P>(rp, qo + 16u, sp);
+    r.a[0] = a0.x, r.a[1] = a0.y, r.a[2] = a0.z, r.a[3] = a0.w;
+    r.a[4] = a1.x, r.a[5] = a1.y, r.a[6] = a1.z, r.a[7] = a1.w;
+    const u32x4 hh = bld_u128<P>(hr, ho, hs);
+    r.h[0] = hh.x, r.h[1] = hh.y, r.h[2] = hh.z, r.h[3] = hh.w;
+  }
+}
+
+__device__ __forceinline__ half8 as_half8(const uint4& u) { return __builtin_bit_cast(half8, u); }
+__device__ __forceinline__ uint4 as_uint4(const half8& h) { return __builtin_bit_cast(uint4, h); }
+
+// Two fp16 integers from two 5-bit fields already placed in the low bits of
+// each 16-bit half: (1024 + v) has the bit pattern 0x6400 | v, and
+// (1024 + v) * m - 1024 m = v m, rounded once (exact: v m < 2048).
+__device__ __forceinline__ std::uint32_t small_pair_times(std::uint32_t fields, _Float16 m) {
+  typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+  const half2 v = __builtin_bit_cast(half2, fields | 0x64006400u);
+  const half2 mm = {m, m};
+  const half2 c = {static_cast<_Float16>(-1024.0f) * m, static_cast<_Float16>(-1024.0f) * m};
+  return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_fma(v, mm, c));
+}
+
+// A operand of instruction j (values 64 q + 8 j .. + 8 of the block).
+template <int FMT>
+__device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, int j, std::uint32_t q,
+                                           half8& amin) {
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+    const std::uint32_t qsb = (r.a[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    const std::uint32_t qh = (r.h[1] >> (8 * (j >> 2))) & 0xFFu;  // qh of 32-value sub-block 2 q + j / 4
+    const std::uint32_t idx = qsb | (((qh >> (2 * (j & 3))) & 3u) << 8);
+    const std::uint32_t sgb = (r.a[2 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
+    const uint4 g = t->grid2h[idx];
+    const uint4 sm = t->sign16[sgb];
+    const std::uint32_t nib = ((r.h[2] >> (8 * (j >> 2))) >> (4 * ((j & 3) >> 1))) & 15u;
+    const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
+    const half8 a = as_half8(make_uint4(g.x ^ sm.x, g.y ^ sm.y, g.z ^ sm.z, g.w ^ sm.w));
+    return a * m;
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
+    const std::uint32_t sub = static_cast<std::uint32_t>(j >> 2);          // 32-value sub-block 2 q + sub
+    const std::uint32_t qh = (r.h[1] >> (8 * sub)) & 0xFFu;
+    const int sel0 = 2 * (j & 3), sel1 = sel0 + 1;                         // qs bytes of this group
+    const std::uint32_t w16 = r.a[(2 * j) >> 2] >> (8 * ((2 * j) & 3));    // qs[2 j], qs[2 j + 1]
+    const std::uint32_t i0 = (w16 & 0xFFu) | (((qh >> sel0) & 1u) << 8);
+    const std::uint32_t i1 = ((w16 >> 8) & 0xFFu) | (((qh >> sel1) & 1u) << 8);
+    const std::uint32_t sgb = (r.a[4 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
+    const uint2 g0 = t->grid3h[i0], g1 = t->grid3h[i1];
+    const uint4 sm = t->sign16[sgb];
+    const std::uint32_t nib = (r.h[2] >> (4u * sub)) & 15u;
+    const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
+    const half8 a = as_half8(make_uint4(g0.x ^ sm.x, g0.y ^ sm.y, g1.x ^ sm.z, g1.y ^ sm.w));
+    return a * m;
+  } else {
+    // K-quants: j < 4 low nibbles of bytes 8 j .. + 8 of the lane's 32 (sub-block
+    // 2 q), j >= 4 high nibbles of bytes 8 (j - 4) .. (sub-block 2 q + 1).
+    const int hi = j >> 2, w = 2 * (j & 3);
+    const std::uint32_t sc03 = r.h[1] & 0x3F3F3F3Fu;
+    const std::uint32_t m03 = r.h[2] & 0x3F3F3F3Fu;
+    const std::uint32_t sc47 = (r.h[3] & 0x0F0F0F0Fu) | ((r.h[1] >> 2) & 0x30303030u);
+    const std::uint32_t m47 = ((r.h[3] >> 4) & 0x0F0F0F0Fu) | ((r.h[2] >> 2) & 0x30303030u);
+    const std::uint32_t pair = 2u * q + static_cast<std::uint32_t>(hi);   // sub-block 0..7
+    const std::uint32_t scw = pair < 4u ? sc03 : sc47, mw = pair < 4u ? m03 : m47;
+    const std::uint32_t sc = (scw >> (8u * (pair & 3u))) & 0xFFu, mn = (mw >> (8u * (pair & 3u))) & 0xFFu;
+    const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
+    const _Float16 mf = static_cast<_Float16>(static_cast<float>(mn));
+    amin = half8{mf, mf, mf, mf, mf, mf, mf, mf};
+    std::uint32_t out[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const std::uint32_t word = r.a[w + k] >> (4 * hi);  // 4 codes in the low nibble of each byte
+      std::uint32_t lo2 = __builtin_amdgcn_perm(0u, word, 0x0C010C00u) & 0x000F000Fu;  // bytes 0, 1
+      std::uint32_t hi2 = __builtin_amdgcn_perm(0u, word, 0x0C030C02u) & 0x000F000Fu;  // bytes 2, 3
+      if constexpr (FMT == RTXLLM_FMT_Q5K) {
+        const std::uint32_t qb = (r.b[w + k] >> pair) & 0x01010101u;  // bit `pair` of each qh byte
+        lo2 |= (__builtin_amdgcn_perm(0u, qb, 0x0C010C00u) << 4);
+        hi2 |= (__builtin_amdgcn_perm(0u, qb, 0x0C030C02u) << 4);
+      }
+      out[2 * k] = small_pair_times(lo2, scf);
+      out[2 * k + 1] = small_pair_times(hi2, scf);
+    }
+    return as_half8(make_uint4(out[0], out[1], out[2], out[3]));
+  }
+}
+
+// d (and dmin) of the block for the lane's row, as fp32.
+// (IQ2_S: d (0.5 + n) / 4 = d / 8 * (2 n + 1), the 2 n + 1 being in A.)
+template <int FMT>
+__device__ __forceinline__ void mm_block_scale(const MmRaw& r, float& d, float& dmin) {
+  d = h2f(r.h[0]);
+  if constexpr (FMT == RTXLLM_FMT_IQ2S) d *= 0.125f;
+  dmin = fmt_is_iq(FMT) ? 0.0f : h2f(r.h[0] >> 16);
+}
+
+// ---- the kernel ----------------------------------------------------------------------
+
+// Grid: x = workgroups over 16-row tiles (persistent), y = panel group of
+// blockDim.x / 64 panels. Writes out[pg][s][r] (row stride out_stride) for
+// s < batch: y itself with one panel group, else per-group partial sums.
+template <int FMT>
+__global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const void* __restrict__ x16,
+                                                             std::uint32_t batch, float* __restrict__ out,
+                                                             std::uint32_t out_stride) {
+  __shared__ float red[kMaxPanels][64][4];
+  const std::uint32_t lane = threadIdx.x & 63u;
+  const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const std::uint32_t nw = blockDim.x >> 6;
+  const std::uint32_t panel = blockIdx.y * nw + wave;  // the launcher makes nw divide the panel count
+  const std::uint32_t cols = w.cols, rows = w.rows, bpr = cols >> 8;
+  const std::uint32_t q = lane >> 4, r16 = lane & 15u, n = lane & 15u;
+  const std::uint32_t tiles = (rows + 15u) >> 4;
+
+  // B operands of the panel: 2 blocks x 8 instructions.
+  const _Float16* xh = static_cast<const _Float16*>(x16);
+  uint4 B[2][8];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const std::uint32_t k = panel * kPanel + 256u * b + 64u * q + 8u * j;
+      B[b][j] = *reinterpret_cast<const uint4*>(xh + static_cast<std::size_t>(n) * cols + k);
+    }
+
+  const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
+  const Rsrc rsp = make_rsrc(w.payload, rows * prow);
+  const Rsrc rsm = make_rsrc(FmtBytes<FMT>::meta > 0u ? w.meta : w.payload, rows * mrow);
+
+  const MmLds<FMT>* tables = nullptr;
+  if constexpr (fmt_is_iq(FMT)) {
+    MmLds<FMT>& t = mm_lds<FMT>();
+    mm_lds_fetch<FMT>(t, wave, lane);
+    tables = &t;
+  }
+
+  // (tile, block) units of this wave in order: unit u -> tile blockIdx.x +
+  // (u / 2) * gridDim.x, block 2 panel + u % 2.
+  const std::uint32_t rounds = (tiles + gridDim.x - 1u) / gridDim.x;
+  auto load_unit = [&](std::uint32_t u, MmRaw& raw) {
+    const std::uint32_t tile = __builtin_amdgcn_readfirstlane(blockIdx.x + (u >> 1) * gridDim.x);
+    if (tile >= tiles) return;
+    std::uint32_t row = tile * 16u + r16;
+    row = row < rows ? row : rows - 1u;
+    mm_load<FMT>(rsp, rsm, row * prow, row * mrow, 2u * panel + (u & 1u), q, raw);
+  };
+  MmRaw ra, rb;
+  load_unit(0u, ra);
+  if constexpr (fmt_is_iq(FMT)) __syncthreads();
+
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto finish_unit = [&](std::uint32_t u, const MmRaw& raw) {
+    const int b = static_cast<int>(u & 1u);
+    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f}, cm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      half8 amin;
+      const half8 a = mm_decode<FMT>(raw, tables, j, q, amin);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, as_half8(B[b][j]), c, 0, 0, 0);
+      if constexpr (!fmt_is_iq(FMT)) cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, as_half8(B[b][j]), cm, 0, 0, 0);
+    }
+    // the C rows of this lane are 4 (l / 16) + i; their scales live in the
+    // lanes that loaded those rows (lane = row, q = 0)
+    float d, dmin;
+    mm_block_scale<FMT>(raw, d, dmin);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int src = static_cast<int>(4u * q) + i;
+      const float di = __shfl(d, src, 64);
+      acc[i] = __builtin_fmaf(c[i], di, acc[i]);
+      if constexpr (!fmt_is_iq(FMT)) acc[i] = __builtin_fmaf(-cm[i], __shfl(dmin, src, 64), acc[i]);
+    }
+  };
+
+  const std::uint32_t units = 2u * rounds;
+  for (std::uint32_t u = 0; u < units; u += 2u) {
+    // unit u: first block of tile round u / 2
+    load_unit(u + 1u, rb);
+    finish_unit(u, ra);
+    load_unit(u + 2u, ra);
+    finish_unit(u + 1u, rb);
+    // tile done: combine the workgroup's panels
+    const std::uint32_t tile = blockIdx.x + (u >> 1) * gridDim.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][lane][i] = acc[i];
+    __syncthreads();
+    if (wave == 0u && tile < tiles) {
+      f32x4 v = acc;
+      for (std::uint32_t k = 1; k < nw; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += red[k][lane][i];
+      // column n = 2 s + h: hi + lo of sequence s (lanes l, l ^ 1)
+      const int* e = reinterpret_cast<const int*>(xh + 16u * static_cast<std::size_t>(cols));
+      const std::uint32_t s = n >> 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float tot = v[i] + __shfl_xor(v[i], 1, 64);
+        const std::uint32_t row = tile * 16u + 4u * q + static_cast<std::uint32_t>(i);
+        if ((n & 1u) == 0u && s < batch && row < rows)
+          out[static_cast<std::size_t>(blockIdx.y) * batch * out_stride + static_cast<std::size_t>(s) * out_stride +
+              row] = ldexpf(tot, e[s]);
+      }
+    }
+    __syncthreads();
+    acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+}
+
+// y[s][r] = sum over panel groups of partial[pg][s][r].
+__global__ void mm_reduce_kernel(const float* __restrict__ partial, std::uint32_t groups, std::uint32_t n,
+                                 float* __restrict__ y) {
+  const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (std::uint32_t g = 0; g < groups; ++g) s += partial[static_cast<std::size_t>(g) * n + i];
+  y[i] = s;
+}
+
+}  // namespace rtxllm

@@ -36,6 +36,8 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_matvec": [c_int, _P, _P, _P, _P, _U, _U, _S],
     "rtxllm_stage_activation": [_P, _P, _U, _P, _S],
     "rtxllm_matvec_xq": [c_int, _P, _P, _P, _P, _U, _U, _S],
+    "rtxllm_stage_batch": [_P, _U, _U, _P, _S],
+    "rtxllm_matvec_batch": [c_int, _P, _P, _P, _P, _U, _U, _U, _P, c_size_t, _S],
     "rtxllm_llama_create": [_P, _P],
     "rtxllm_llama_upload": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
     "rtxllm_llama_download": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
@@ -70,6 +72,8 @@ _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_format_payload_block_bytes": (c_uint32, [c_int]),
     "rtxllm_format_meta_block_bytes": (c_uint32, [c_int]),
     "rtxllm_xq_bytes": (c_size_t, [c_uint32]),
+    "rtxllm_x16_bytes": (c_size_t, [c_uint32]),
+    "rtxllm_matvec_batch_workspace": (c_size_t, [c_int, c_uint32, c_uint32]),
     "rtxllm_llama_destroy": (None, [_P]),
     "rtxllm_llama_region": (_P, [_P, ctypes.c_char_p, _U, _P]),
     "rtxllm_llama_launches_per_step": (c_uint32, [_P]),

@@ -93,3 +93,42 @@ def matvec_xq(w: DevicePack, xq: torch.Tensor, y: torch.Tensor | None = None) ->
     check("rtxllm_matvec_xq", lib().rtxllm_matvec_xq(w.fmt, ptr(w.payload), ptr(w.meta), ptr(xq), ptr(y), w.rows,
                                                       w.cols, stream()))
     return y
+
+
+# ---- batched matvec (1..8 activation vectors, matrix cores) -------------------------
+
+BATCH_MAX = 8
+
+
+def x16_bytes(cols: int) -> int:
+    return int(lib().rtxllm_x16_bytes(cols))
+
+
+def stage_batch(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x: device fp32 [batch, cols] -> the staged fp16 hi/lo buffer (uint8)."""
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("expected a contiguous device fp32 [batch, cols] tensor")
+    batch, cols = x.shape
+    if out is None:
+        out = torch.empty(x16_bytes(cols), dtype=torch.uint8, device=x.device)
+    if out.numel() < x16_bytes(cols):
+        raise ValueError("staging buffer smaller than rtxllm_x16_bytes(cols)")
+    check("rtxllm_stage_batch", lib().rtxllm_stage_batch(ptr(x), batch, cols, ptr(out), stream()))
+    return out
+
+
+def matvec_batch(w: DevicePack, x16: torch.Tensor, batch: int, y: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y [batch, rows] = W x_s for the staged activations."""
+    if x16.dtype != torch.uint8 or x16.numel() < x16_bytes(w.cols) or not x16.is_cuda:
+        raise ValueError("expected a device staging buffer of rtxllm_x16_bytes(cols) bytes")
+    if y is None:
+        y = torch.empty((batch, w.rows), dtype=torch.float32, device=x16.device)
+    _check_vec(y, batch * w.rows)
+    need = int(lib().rtxllm_matvec_batch_workspace(w.fmt, w.rows, w.cols))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x16.device)
+    check("rtxllm_matvec_batch", lib().rtxllm_matvec_batch(w.fmt, ptr(w.payload), ptr(w.meta), ptr(x16), ptr(y),
+                                                            w.rows, w.cols, batch,
+                                                            ptr(workspace) if need else None, need, stream()))
+    return y
