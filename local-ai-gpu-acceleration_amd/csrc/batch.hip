@@ -8,16 +8,18 @@ namespace rtxllm {
 namespace {
 
 // One workgroup per sequence: e_s from max |x_s|, then the hi / lo fp16 pair
-// of x_s 2^-e_s. Sequences >= batch get zero columns.
+// of x_s 2^-e_s, each at its place in the operand order (x16_index).
+// Sequences >= batch get zero columns.
 __global__ __launch_bounds__(1024) void stage_batch_kernel(const float* __restrict__ x, std::uint32_t batch,
                                                            std::uint32_t cols, _Float16* __restrict__ x16) {
   __shared__ float part[16];
   const std::uint32_t s = blockIdx.x;
   int* e_out = reinterpret_cast<int*>(x16 + 16u * static_cast<std::size_t>(cols));
-  _Float16* hi = x16 + static_cast<std::size_t>(2u * s) * cols;
-  _Float16* lo = hi + cols;
   if (s >= batch) {
-    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) hi[c] = lo[c] = static_cast<_Float16>(0.0f);
+    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
+      const std::size_t i = x16_index(2u * s, c);
+      x16[i] = x16[i + 8u] = static_cast<_Float16>(0.0f);
+    }
     if (threadIdx.x == 0u) e_out[s] = 0;
     return;
   }
@@ -35,10 +37,39 @@ __global__ __launch_bounds__(1024) void stage_batch_kernel(const float* __restri
   for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
     const float v = ldexpf(xs[c], -e);
     const _Float16 h = static_cast<_Float16>(v);
-    hi[c] = h;
-    lo[c] = static_cast<_Float16>(v - static_cast<float>(h));
+    const std::size_t i = x16_index(2u * s, c);
+    x16[i] = h;
+    x16[i + 8u] = static_cast<_Float16>(v - static_cast<float>(h));  // column 2 s + 1: lane + 1
   }
   if (threadIdx.x == 0u) e_out[s] = e;
+}
+
+// Workgroups of mm_kernel<FMT> of `threads` threads resident per CU (0 if the
+// query fails), cached per format and size.
+template <int FMT>
+int mm_resident_fmt(std::uint32_t threads) {
+  static int cache[kMaxPanels + 1] = {};
+  const std::uint32_t w = threads / 64u;
+  if (w == 0u || w > kMaxPanels) return 0;
+  if (cache[w] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mm_kernel<FMT>),
+                                                     static_cast<int>(threads), 0) != hipSuccess || n <= 0)
+      return 0;
+    cache[w] = n;
+  }
+  return cache[w];
+}
+
+inline int mm_resident(int fmt, std::uint32_t threads) {
+  switch (fmt) {
+    case RTXLLM_FMT_IQ2S: return mm_resident_fmt<RTXLLM_FMT_IQ2S>(threads);
+    case RTXLLM_FMT_IQ3S: return mm_resident_fmt<RTXLLM_FMT_IQ3S>(threads);
+    case RTXLLM_FMT_Q5K: return mm_resident_fmt<RTXLLM_FMT_Q5K>(threads);
+    case RTXLLM_FMT_Q4K_RAW: return mm_resident_fmt<RTXLLM_FMT_Q4K_RAW>(threads);
+    case RTXLLM_FMT_Q4K_SPLIT_NATIVE: return mm_resident_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(threads);
+    default: return 0;
+  }
 }
 
 struct MmGeom {
@@ -56,9 +87,13 @@ inline bool mm_geom(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) 
     }
   g.groups = panels / g.ppg;
   const std::uint32_t tiles = (rows + 15u) / 16u;
-  // persistent: at most 2 workgroups of up to 8 waves per CU per panel group
-  const std::uint32_t cap = 2u * static_cast<std::uint32_t>(num_cus()) / g.groups + 1u;
-  g.grid = tiles < cap ? tiles : cap;
+  // persistent: the workgroups resident at once, shared by the panel groups,
+  // every workgroup taking the same number of tiles (but the last few)
+  const int resident = mm_resident(fmt, 64u * g.ppg);
+  const std::uint32_t per_cu = resident > 0 ? static_cast<std::uint32_t>(resident) : 1u;
+  const std::uint32_t cap = std::max(1u, per_cu * static_cast<std::uint32_t>(num_cus()) / g.groups);
+  const std::uint32_t rounds = (tiles + cap - 1u) / cap;
+  g.grid = (tiles + rounds - 1u) / rounds;
   return true;
 }
 

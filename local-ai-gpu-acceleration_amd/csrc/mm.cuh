@@ -41,10 +41,18 @@ constexpr std::uint32_t kBatchMax = 8;
 constexpr std::uint32_t kPanel = 512;        // columns per wave
 constexpr std::uint32_t kMaxPanels = 8;      // waves per workgroup
 
-// Staged batch activation: x16[n][cols] fp16 (n = 2 s + h, 16 columns), then
-// int32 e[8].
+// Staged batch activation: 16 fp16 columns X[n] (n = 2 s + hi/lo) of cols
+// values in operand order (x16_index), then int32 e[8].
 __host__ __device__ inline std::size_t x16_bytes(std::uint32_t cols) {
   return 32u * static_cast<std::size_t>(cols) + 4u * kBatchMax;
+}
+
+// Index (in fp16 values) of X[n][c]: the place where lane l = 16 (k / 64) + n
+// of instruction j = k / 8 % 8 of block kb = c / 256 holds its eight B values
+// (k = c % 256, value i = k % 8).
+__host__ __device__ inline std::size_t x16_index(std::uint32_t n, std::uint32_t c) {
+  const std::uint32_t k = c & 255u;
+  return ((static_cast<std::size_t>(c >> 8) * 8u + ((k >> 3) & 7u)) * 64u + 16u * (k >> 6) + n) * 8u + (k & 7u);
 }
 
 constexpr bool fmt_mm_supported(int f) {
@@ -136,44 +144,48 @@ __device__ __forceinline__ void mm_lds_fetch(MmLds<FMT>& t, std::uint32_t wave, 
 struct MmRaw {
   std::uint32_t a[8];  // IQ2_S: qs[0..1] signs[2..3]; IQ3_S: qs[0..3] signs[4..5]; K: quants (32 B)
   std::uint32_t b[8];  // Q5_K: qh (32 B)
-  std::uint32_t h[4];  // K: the 16 B head (d, dmin, scales); IQ: [0] d, [1] qh pair, [2] scale byte(s)
+  std::uint32_t h[4];  // K: the 16 B head (d, dmin, scales)
+  // IQ: d, the qh pair, the scale pair (IQ2_S) or byte (IQ3_S), kept at their
+  // loaded width so their zero extension happens where they are used
+  std::uint16_t s[3];
+  std::uint8_t s8;
 };
 
 template <int FMT>
-__device__ __forceinline__ void mm_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, std::uint32_t blk,
-                                        std::uint32_t q, MmRaw& r) {
+__device__ __forceinline__ void mm_load(Rsrc rp, Rsrc rm, std::uint32_t vp, std::uint32_t vm, std::uint32_t sp,
+                                        std::uint32_t sm, std::uint32_t blk, std::uint32_t q, MmRaw& r) {
   constexpr int P = load_policy<FMT>();
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    const std::uint32_t o = blk * 82u;
+    const std::uint32_t o = vp + blk * 82u;
     const u32x2 qs = bld_u64<P>(rp, o + 2u + 8u * q, sp);
     const u32x2 sg = bld_u64<P>(rp, o + 34u + 8u * q, sp);
     r.a[0] = qs.x, r.a[1] = qs.y, r.a[2] = sg.x, r.a[3] = sg.y;
-    r.h[0] = bld_u16<P>(rp, o, sp);
-    r.h[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
-    r.h[2] = bld_u16<P>(rp, o + 74u + 2u * q, sp);
+    r.s[0] = bld_u16<P>(rp, o, sp);
+    r.s[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
+    r.s[2] = bld_u16<P>(rp, o + 74u + 2u * q, sp);
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
-    const std::uint32_t o = blk * 110u;
+    const std::uint32_t o = vp + blk * 110u;
     const u32x2 q0 = bld_u64<P>(rp, o + 2u + 16u * q, sp);
     const u32x2 q1 = bld_u64<P>(rp, o + 10u + 16u * q, sp);
     const u32x2 sg = bld_u64<P>(rp, o + 74u + 8u * q, sp);
     r.a[0] = q0.x, r.a[1] = q0.y, r.a[2] = q1.x, r.a[3] = q1.y, r.a[4] = sg.x, r.a[5] = sg.y;
-    r.h[0] = bld_u16<P>(rp, o, sp);
-    r.h[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
-    r.h[2] = bld_u8<P>(rp, o + 106u + q, sp);
+    r.s[0] = bld_u16<P>(rp, o, sp);
+    r.s[1] = bld_u16<P>(rp, o + 66u + 2u * q, sp);
+    r.s8 = bld_u8<P>(rp, o + 106u + q, sp);
   } else {
     std::uint32_t qo, ho;
     Rsrc hr = rp;
     std::uint32_t hs = sp;
     if constexpr (FMT == RTXLLM_FMT_Q5K) {
-      qo = blk * 176u + 48u + 32u * q, ho = blk * 176u;
-      const u32x4 h0 = bld_u128<P>(rp, blk * 176u + 16u, sp);
-      const u32x4 h1 = bld_u128<P>(rp, blk * 176u + 32u, sp);
+      qo = vp + blk * 176u + 48u + 32u * q, ho = vp + blk * 176u;
+      const u32x4 h0 = bld_u128<P>(rp, ho + 16u, sp);
+      const u32x4 h1 = bld_u128<P>(rp, ho + 32u, sp);
       r.b[0] = h0.x, r.b[1] = h0.y, r.b[2] = h0.z, r.b[3] = h0.w;
       r.b[4] = h1.x, r.b[5] = h1.y, r.b[6] = h1.z, r.b[7] = h1.w;
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_RAW) {
-      qo = blk * 144u + 16u + 32u * q, ho = blk * 144u;
+      qo = vp + blk * 144u + 16u + 32u * q, ho = vp + blk * 144u;
     } else {  // split-native: 128 B payload, 16 B head in the metadata stream
-      qo = blk * 128u + 32u * q, ho = blk * 16u;
+      qo = vp + blk * 128u + 32u * q, ho = vm + blk * 16u;
       hr = rm, hs = sm;
     }
     const u32x4 a0 = bld_u128<P>(rp, qo, sp);
@@ -205,18 +217,18 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
                                            half8& amin) {
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
     const std::uint32_t qsb = (r.a[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-    const std::uint32_t qh = (r.h[1] >> (8 * (j >> 2))) & 0xFFu;  // qh of 32-value sub-block 2 q + j / 4
+    const std::uint32_t qh = (std::uint32_t{r.s[1]} >> (8 * (j >> 2))) & 0xFFu;  // qh of sub-block 2 q + j / 4
     const std::uint32_t idx = qsb | (((qh >> (2 * (j & 3))) & 3u) << 8);
     const std::uint32_t sgb = (r.a[2 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
     const uint4 g = t->grid2h[idx];
     const uint4 sm = t->sign16[sgb];
-    const std::uint32_t nib = ((r.h[2] >> (8 * (j >> 2))) >> (4 * ((j & 3) >> 1))) & 15u;
+    const std::uint32_t nib = ((std::uint32_t{r.s[2]} >> (8 * (j >> 2))) >> (4 * ((j & 3) >> 1))) & 15u;
     const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
     const half8 a = as_half8(make_uint4(g.x ^ sm.x, g.y ^ sm.y, g.z ^ sm.z, g.w ^ sm.w));
     return a * m;
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
     const std::uint32_t sub = static_cast<std::uint32_t>(j >> 2);          // 32-value sub-block 2 q + sub
-    const std::uint32_t qh = (r.h[1] >> (8 * sub)) & 0xFFu;
+    const std::uint32_t qh = (std::uint32_t{r.s[1]} >> (8 * sub)) & 0xFFu;
     const int sel0 = 2 * (j & 3), sel1 = sel0 + 1;                         // qs bytes of this group
     const std::uint32_t w16 = r.a[(2 * j) >> 2] >> (8 * ((2 * j) & 3));    // qs[2 j], qs[2 j + 1]
     const std::uint32_t i0 = (w16 & 0xFFu) | (((qh >> sel0) & 1u) << 8);
@@ -224,7 +236,7 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
     const std::uint32_t sgb = (r.a[4 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
     const uint2 g0 = t->grid3h[i0], g1 = t->grid3h[i1];
     const uint4 sm = t->sign16[sgb];
-    const std::uint32_t nib = (r.h[2] >> (4u * sub)) & 15u;
+    const std::uint32_t nib = (std::uint32_t{r.s8} >> (4u * sub)) & 15u;
     const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
     const half8 a = as_half8(make_uint4(g0.x ^ sm.x, g0.y ^ sm.y, g1.x ^ sm.z, g1.y ^ sm.w));
     return a * m;
@@ -264,39 +276,70 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
 // (IQ2_S: d (0.5 + n) / 4 = d / 8 * (2 n + 1), the 2 n + 1 being in A.)
 template <int FMT>
 __device__ __forceinline__ void mm_block_scale(const MmRaw& r, float& d, float& dmin) {
-  d = h2f(r.h[0]);
-  if constexpr (FMT == RTXLLM_FMT_IQ2S) d *= 0.125f;
-  dmin = fmt_is_iq(FMT) ? 0.0f : h2f(r.h[0] >> 16);
+  if constexpr (fmt_is_iq(FMT)) {
+    d = h2f(r.s[0]);
+    if constexpr (FMT == RTXLLM_FMT_IQ2S) d *= 0.125f;
+    dmin = 0.0f;
+  } else {
+    d = h2f(r.h[0]);
+    dmin = h2f(r.h[0] >> 16);
+  }
 }
 
 // ---- the kernel ----------------------------------------------------------------------
 
-// Grid: x = workgroups over 16-row tiles (persistent), y = panel group of
-// blockDim.x / 64 panels. Writes out[pg][s][r] (row stride out_stride) for
-// s < batch: y itself with one panel group, else per-group partial sums.
+// f(integral_constant<int, I>) for I = 0 .. N - 1, unrolled at compile time.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// Depth of the per-wave ring of block loads in flight (units issued ahead of
+// the one being computed = depth - 1); the wider the lane's fields, the shallower.
+template <int FMT>
+constexpr int mm_ring() {
+  return FMT == RTXLLM_FMT_Q5K ? 2 : (fmt_is_iq(FMT) ? 4 : 3);
+}
+
+// Grid: x = workgroups over 16-row tiles (persistent: workgroup g takes tiles
+// g, g + gridDim.x, ...), y = panel group of blockDim.x / 64 panels. Writes
+// out[pg][s][r] (row stride out_stride) for s < batch: y itself with one panel
+// group, else per-group partial sums.
 template <int FMT>
 __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const void* __restrict__ x16,
                                                              std::uint32_t batch, float* __restrict__ out,
                                                              std::uint32_t out_stride) {
-  __shared__ float red[kMaxPanels][64][4];
+  // per-panel partial C of a tile, double buffered by tile parity
+  __shared__ float red[2][kMaxPanels][256];
   const std::uint32_t lane = threadIdx.x & 63u;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::uint32_t nw = blockDim.x >> 6;
   const std::uint32_t panel = blockIdx.y * nw + wave;  // the launcher makes nw divide the panel count
   const std::uint32_t cols = w.cols, rows = w.rows, bpr = cols >> 8;
-  const std::uint32_t q = lane >> 4, r16 = lane & 15u, n = lane & 15u;
+  const std::uint32_t q = lane >> 4, r16 = lane & 15u;
   const std::uint32_t tiles = (rows + 15u) >> 4;
 
-  // B operands of the panel: 2 blocks x 8 instructions.
+  // B operands of the panel: 2 blocks x 8 instructions, 1 KB of whole lanes each.
   const _Float16* xh = static_cast<const _Float16*>(x16);
+  const uint4* xb = reinterpret_cast<const uint4*>(x16) + 2u * panel * 8u * 64u + lane;
   uint4 B[2][8];
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const std::uint32_t k = panel * kPanel + 256u * b + 64u * q + 8u * j;
-      B[b][j] = *reinterpret_cast<const uint4*>(xh + static_cast<std::size_t>(n) * cols + k);
-    }
+    for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
+
+  // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
+  // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
+  // n = l % 16 = 2 s + hi/lo. blockDim.x being a multiple of 64, n and s are
+  // the same for all of a thread's elements.
+  const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
+  const bool t_store = (t_n & 1u) == 0u && t_s < batch;
+  const int t_e = reinterpret_cast<const int*>(xh + 16u * static_cast<std::size_t>(cols))[t_s];
+  float* const t_out = out + static_cast<std::size_t>(blockIdx.y) * batch * out_stride +
+                       static_cast<std::size_t>(t_s) * out_stride;
 
   const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
   const Rsrc rsp = make_rsrc(w.payload, rows * prow);
@@ -310,17 +353,24 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   }
 
   // (tile, block) units of this wave in order: unit u -> tile blockIdx.x +
-  // (u / 2) * gridDim.x, block 2 panel + u % 2.
-  const std::uint32_t rounds = (tiles + gridDim.x - 1u) / gridDim.x;
+  // (u / 2) * gridDim.x, block 2 panel + u % 2. Loads past the workgroup's
+  // last unit re-read that unit (no branch around the loads, so the waits on
+  // the ring stay exact counts).
+  const std::uint32_t rounds = blockIdx.x < tiles ? (tiles - blockIdx.x + gridDim.x - 1u) / gridDim.x : 0u;
+  const std::uint32_t units = 2u * rounds;
   auto load_unit = [&](std::uint32_t u, MmRaw& raw) {
-    const std::uint32_t tile = __builtin_amdgcn_readfirstlane(blockIdx.x + (u >> 1) * gridDim.x);
-    if (tile >= tiles) return;
-    std::uint32_t row = tile * 16u + r16;
-    row = row < rows ? row : rows - 1u;
-    mm_load<FMT>(rsp, rsm, row * prow, row * mrow, 2u * panel + (u & 1u), q, raw);
+    u = u < units ? u : units - 1u;
+    const std::uint32_t row0 = __builtin_amdgcn_readfirstlane((blockIdx.x + (u >> 1) * gridDim.x) * 16u);
+    // the tile's first row in the uniform offset, the lane's row within the
+    // tile (clamped to the last row) in the per-lane offset
+    const std::uint32_t r = min(r16, rows - 1u - row0);
+    mm_load<FMT>(rsp, rsm, r * prow, r * mrow, row0 * prow, row0 * mrow, 2u * panel + (u & 1u), q, raw);
   };
-  MmRaw ra, rb;
-  load_unit(0u, ra);
+  if (units == 0u) return;  // whole workgroup: no barrier is left waiting
+  constexpr int NB = mm_ring<FMT>();
+  MmRaw ring[NB];
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j) load_unit(static_cast<std::uint32_t>(j), ring[j]);
   if constexpr (fmt_is_iq(FMT)) __syncthreads();
 
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -346,39 +396,40 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       if constexpr (!fmt_is_iq(FMT)) acc[i] = __builtin_fmaf(-cm[i], __shfl(dmin, src, 64), acc[i]);
     }
   };
-
-  const std::uint32_t units = 2u * rounds;
-  for (std::uint32_t u = 0; u < units; u += 2u) {
-    // unit u: first block of tile round u / 2
-    load_unit(u + 1u, rb);
-    finish_unit(u, ra);
-    load_unit(u + 2u, ra);
-    finish_unit(u + 1u, rb);
-    // tile done: combine the workgroup's panels
-    const std::uint32_t tile = blockIdx.x + (u >> 1) * gridDim.x;
+  // tile done: every panel's partial to LDS, one barrier, then each of the 256
+  // C elements summed over the panels and hi + lo of a sequence written.
+  auto tile_end = [&](std::uint32_t round) {
+    float* const mine = red[round & 1u][wave];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][lane][i] = acc[i];
-    __syncthreads();
-    if (wave == 0u && tile < tiles) {
-      f32x4 v = acc;
-      for (std::uint32_t k = 1; k < nw; ++k)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += red[k][lane][i];
-      // column n = 2 s + h: hi + lo of sequence s (lanes l, l ^ 1)
-      const int* e = reinterpret_cast<const int*>(xh + 16u * static_cast<std::size_t>(cols));
-      const std::uint32_t s = n >> 1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float tot = v[i] + __shfl_xor(v[i], 1, 64);
-        const std::uint32_t row = tile * 16u + 4u * q + static_cast<std::uint32_t>(i);
-        if ((n & 1u) == 0u && s < batch && row < rows)
-          out[static_cast<std::size_t>(blockIdx.y) * batch * out_stride + static_cast<std::size_t>(s) * out_stride +
-              row] = ldexpf(tot, e[s]);
-      }
-    }
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) mine[4u * lane + static_cast<std::uint32_t>(i)] = acc[i];
     acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+    __syncthreads();
+    for (std::uint32_t e = threadIdx.x; e < 256u; e += blockDim.x) {  // whole waves
+      float v = 0.0f;
+      for (std::uint32_t k = 0; k < nw; ++k) v += red[round & 1u][k][e];
+      const float tot = v + __shfl_xor(v, 4, 64);  // column n ^ 1 is lane l ^ 1 = element e ^ 4
+      const std::uint32_t row = (blockIdx.x + round * gridDim.x) * 16u + 4u * (e >> 6) + (e & 3u);
+      if (t_store && row < rows) t_out[row] = ldexpf(tot, t_e);
+    }
+  };
+
+  // unit u sits in ring slot u % NB; PERIOD units bring both the slot and the
+  // block parity back. The main loop's body runs whole (no exit inside it, so
+  // the waits on the ring stay exact counts); the tail runs what is left.
+  constexpr int PERIOD = NB % 2 == 0 ? NB : 2 * NB;
+  auto step = [&](std::uint32_t u, auto jc) {
+    constexpr int j = decltype(jc)::value;
+    load_unit(u + NB - 1u, ring[(j + NB - 1) % NB]);
+    __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this unit's work
+    finish_unit(u, ring[j % NB]);
+    if constexpr (j % 2 == 1) tile_end(u >> 1);
+  };
+  std::uint32_t u0 = 0;
+  for (; u0 + PERIOD <= units; u0 += PERIOD)
+    static_for<PERIOD>([&](auto jc) { step(u0 + decltype(jc)::value, jc); });
+  static_for<PERIOD>([&](auto jc) {
+    if (u0 + decltype(jc)::value < units) step(u0 + decltype(jc)::value, jc);
+  });
 }
 
 // y[s][r] = sum over panel groups of partial[pg][s][r].
