@@ -1,9 +1,12 @@
-/* C-ABI of the MI355X Llama decode runner (batch 1): one resident VRAM arena
- * holding every layer's packs, the fp16 paged KV cache and the workspace; one
- * decode step = embedding gather, per layer {fused qkv matvec + RoPE + KV
- * append, split-context GQA attention, o matvec + residual + ffn-norm staging,
- * fused gate/up matvec + SiLU-gate, down matvec + residual + next-norm
- * staging}, final norm + LM head + greedy argmax; replayable as one hipGraph.
+/* C-ABI of the MI355X Llama decode runner (batch 1, or 2..8 sequences): one
+ * resident VRAM arena holding every layer's packs, the fp16 paged KV cache and
+ * the workspace; one decode step = embedding gather, per layer {fused qkv
+ * matvec + RoPE + KV append, split-context GQA attention, o matvec + residual
+ * + ffn-norm staging, fused gate/up matvec + SiLU-gate, down matvec + residual
+ * + next-norm staging}, final norm + LM head + greedy argmax; replayable as one
+ * hipGraph. A batch step runs every sequence through the same weights once,
+ * on the matrix cores (each sequence with its own token, position and KV
+ * pages).
  *
  * No counterpart in the reference: its layer-slice runner
  * (runtime/apps/mixed_sequence_benchmark_runner/main.cpp:3136-5818) drives
@@ -38,6 +41,9 @@ typedef struct {
   int fmt_gate_up;     /* embedding table is Q5_K */
   int fmt_down;
   int fmt_lm_head;
+  uint32_t batch;      /* sequences per step, 0 or 1: batch 1; 2..8: the batch
+                          step (hidden % 512 == 0 and <= 4096, n_heads % 4 == 0,
+                          ffn % 512 == 0) */
 } rtxllm_llama_config;
 
 typedef struct rtxllm_llama rtxllm_llama;
@@ -54,7 +60,13 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * (int32 [max_ctx / page_size]). Global (layer ignored): "embed", "lm_head",
  * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos",
  * and the work buffers "xq" / "xq_att" (staged activations), "sumsq",
- * "attn_partials", "argkeys", "inv_freq".
+ * "attn_partials", "argkeys", "inv_freq"; with batch > 1 also "x16" (staged
+ * batch activation) and "mm_work" (matvec outputs before the residual).
+ * With batch B > 1 the per-sequence regions hold B rows, sequence s at row s:
+ * h [B][hidden], q / att [B][n_heads*128], act [B][ffn], logits [B][vocab],
+ * token / pos [B]; the KV caches hold B * max_ctx / page_size pages and
+ * block_table is [B][max_ctx / page_size] (initially sequence s owns pages
+ * [s * max_ctx / page_size, (s + 1) * max_ctx / page_size)).
  * Row layouts: qkv = q rows (n_heads*128) | k rows | v rows; gate_up rows
  * interleaved (2i = gate_i, 2i+1 = up_i). */
 void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes);
@@ -75,8 +87,9 @@ hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_
 
 enum { RTXLLM_LLAMA_EMBED = 1, RTXLLM_LLAMA_HEAD = 2 };
 
-/* Layers [first, last) at position *pos. flags & EMBED: h = embed[*token], else
- * h is taken as is. flags & HEAD: final norm, LM head, token = argmax, pos += 1. */
+/* Layers [first, last) at position *pos (per sequence: pos[s]). flags & EMBED:
+ * h = embed[*token], else h is taken as is. flags & HEAD: final norm, LM head,
+ * token = argmax, pos += 1. */
 hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint32_t last, int flags, hipStream_t stream);
 /* One full decode step: forward(0, n_layers, EMBED | HEAD). */
 hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream);

@@ -1,6 +1,14 @@
 // Batched (1..8 activation vectors) matvec entry points on the matrix cores
-// (mm.cuh), and their activation staging.
+// (mm.cuh), their activation staging, and the batch decode step's kernels:
+// residual + RMSNorm + staging per sequence, and the matvec epilogues of the
+// qkv (RoPE + KV append), gate/up (SiLU-gate) and LM-head (logits + argmax
+// keys) projections.
+#include <algorithm>
+
+#include "dequant.cuh"
 #include "internal.h"
+#include "layer.h"
+#include "layer_common.cuh"
 #include "mm.cuh"
 #include "mv_launch.cuh"
 
@@ -44,16 +52,176 @@ __global__ __launch_bounds__(1024) void stage_batch_kernel(const float* __restri
   if (threadIdx.x == 0u) e_out[s] = e;
 }
 
-// Workgroups of mm_kernel<FMT> of `threads` threads resident per CU (0 if the
-// query fails), cached per format and size.
-template <int FMT>
-int mm_resident_fmt(std::uint32_t threads) {
+// Residual + RMSNorm + staging of one batch step, one workgroup per sequence
+// s < batch: v = embed ? dequant(embed[token[s]]) : h[s] (+ the panel groups'
+// partial sums res[g][s] in group order, when res is set); h[s] = v; then x16
+// columns of s = stage(v / sqrt(mean(v^2) + eps) * w).
+struct RmsStageArgs {
+  float* h;              // [batch][cols]
+  const float* res;      // [groups][batch][cols] or null
+  std::uint32_t groups;
+  const std::uint8_t* embed;  // Q5_K [vocab][cols] or null
+  const std::uint32_t* token;
+  std::uint32_t vocab;
+  const float* w;        // [cols] or null
+  float eps;
+  std::uint32_t cols, batch;
+  _Float16* x16;
+};
+
+constexpr std::uint32_t kStageThreads = 1024;
+constexpr std::uint32_t kStagePer = 16;  // values per thread: cols <= 16384
+
+__device__ __forceinline__ float block_reduce(float v, float* part, bool is_max) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float t = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, t) : v + t;
+  }
+  __syncthreads();  // part may still be read by a previous reduction
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = part[0];
+  for (std::uint32_t i = 1; i < blockDim.x / 64u; ++i) r = is_max ? fmaxf(r, part[i]) : r + part[i];
+  return r;
+}
+
+__global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStageArgs a) {
+  __shared__ float part[kStageThreads / 64u];
+  const std::uint32_t s = blockIdx.x, cols = a.cols;
+  float* const hs = a.h + static_cast<std::size_t>(s) * cols;
+  const std::uint8_t* erow = nullptr;
+  if (a.embed != nullptr) {
+    const std::uint32_t tok = a.token[s] < a.vocab ? a.token[s] : a.vocab - 1u;
+    erow = a.embed + static_cast<std::size_t>(tok) * (cols / 256u) * 176u;
+  }
+  float v[kStagePer];
+  float sq = 0.0f;
+#pragma unroll
+  for (std::uint32_t k = 0; k < kStagePer; ++k) {
+    const std::uint32_t c = threadIdx.x + kStageThreads * k;
+    v[k] = 0.0f;
+    if (c >= cols) continue;
+    float x = erow != nullptr ? dequant_value<RTXLLM_FMT_Q5K>(erow + (c / 256u) * 176u, nullptr, c & 255u) : hs[c];
+    if (a.res != nullptr)
+      for (std::uint32_t g = 0; g < a.groups; ++g)
+        x += a.res[(static_cast<std::size_t>(g) * a.batch + s) * cols + c];
+    if (erow != nullptr || a.res != nullptr) hs[c] = x;
+    v[k] = x;
+    sq += x * x;
+  }
+  sq = block_reduce(sq, part, false);
+  const float inv = 1.0f / sqrtf(sq / static_cast<float>(cols) + a.eps);
+  float m = 0.0f;
+#pragma unroll
+  for (std::uint32_t k = 0; k < kStagePer; ++k) {
+    const std::uint32_t c = threadIdx.x + kStageThreads * k;
+    if (c >= cols) continue;
+    v[k] = a.w != nullptr ? v[k] * inv * a.w[c] : v[k] * inv;
+    m = fmaxf(m, fabsf(v[k]));
+  }
+  m = block_reduce(m, part, true);
+  int e = 0;
+  if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);
+#pragma unroll
+  for (std::uint32_t k = 0; k < kStagePer; ++k) {
+    const std::uint32_t c = threadIdx.x + kStageThreads * k;
+    if (c >= cols) continue;
+    const float x = ldexpf(v[k], -e);
+    const _Float16 hi = static_cast<_Float16>(x);
+    const std::size_t i = x16_index(2u * s, c);
+    a.x16[i] = hi;
+    a.x16[i + 8u] = static_cast<_Float16>(x - static_cast<float>(hi));
+  }
+  if (threadIdx.x == 0u) reinterpret_cast<int*>(a.x16 + 16u * static_cast<std::size_t>(cols))[s] = e;
+}
+
+// ---- batch epilogues --------------------------------------------------------
+
+// q | k | v rows (q_rows + 2 kv_rows): RoPE at the sequence's position on q and
+// k (pairs of adjacent rows), q -> q[s], k and v -> the fp16 cache slot of
+// (sequence s, its position); the rule of the batch-1 qkv epilogue.
+struct MmQkv {
+  std::uint32_t q_rows, kv_rows, batch, table_stride;
+  const float* inv_freq;
+  const std::uint32_t* pos_ptr;
+  float* q;
+  KvLayer kv;
+  std::uint32_t pos;
+  __device__ __forceinline__ void init(std::uint32_t s) { pos = s < batch ? pos_ptr[s] : 0u; }
+  __device__ __forceinline__ void operator()(std::uint32_t row, std::uint32_t s, float y, float partner) const {
+    if (row >= q_rows && pos >= kv.capacity) return;  // no slot for this position
+    const std::int32_t* table = kv.block_table + static_cast<std::size_t>(s) * table_stride;
+    if (row < q_rows + kv_rows) {
+      const std::uint32_t d = row & (kHeadDim - 1u);
+      const float angle = static_cast<float>(pos) * inv_freq[d >> 1];
+      const float sn = sinf(angle), cs = cosf(angle);
+      const float out = (d & 1u) ? (partner * sn + y * cs) : (y * cs - partner * sn);
+      if (row < q_rows) {
+        q[static_cast<std::size_t>(s) * q_rows + row] = out;
+      } else {
+        const std::uint32_t kr = row - q_rows;
+        kv.k[kv_offset(kv, table, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
+      }
+    } else {
+      const std::uint32_t vr = row - q_rows - kv_rows;
+      kv.v[kv_offset(kv, table, pos, vr / kHeadDim) + (vr & (kHeadDim - 1u))] = f2h(y);
+    }
+  }
+  __device__ __forceinline__ void finish(std::uint32_t, std::uint32_t, std::uint32_t) {}
+};
+
+// Interleaved gate / up rows: act[s][i] = silu(gate_i) * up_i.
+struct MmGateUp {
+  float* act;
+  std::uint32_t stride;
+  __device__ __forceinline__ void init(std::uint32_t) {}
+  __device__ __forceinline__ void operator()(std::uint32_t row, std::uint32_t s, float y, float partner) const {
+    if ((row & 1u) == 0u) act[static_cast<std::size_t>(s) * stride + (row >> 1)] = silu(y) * partner;
+  }
+  __device__ __forceinline__ void finish(std::uint32_t, std::uint32_t, std::uint32_t) {}
+};
+
+// Logits of every sequence and, per workgroup and sequence, four argmax keys
+// (one per epilogue wave slot) at keys[s * key_stride + 4 blockIdx.x + w].
+// A thread keeps the best key of its rows; lanes 8 s .. 8 s + 3 of a wave are
+// sequence s's.
+struct MmLogits {
+  float* logits;
+  std::uint32_t stride, batch;
+  unsigned long long* keys;
+  std::uint32_t key_stride;
+  unsigned long long best;
+  __device__ __forceinline__ void init(std::uint32_t) { best = 0ull; }
+  __device__ __forceinline__ void operator()(std::uint32_t row, std::uint32_t s, float y, float) {
+    logits[static_cast<std::size_t>(s) * stride + row] = y;
+    const unsigned long long k = argmax_key(y, row);
+    best = k > best ? k : best;
+  }
+  __device__ __forceinline__ void finish(std::uint32_t wave, std::uint32_t lane, std::uint32_t nw) const {
+    unsigned long long k = best, o = __shfl_xor(k, 1, 64);
+    k = o > k ? o : k;
+    o = __shfl_xor(k, 2, 64);
+    k = o > k ? o : k;
+    const std::uint32_t s = (lane >> 3) & 7u;
+    if ((lane & 7u) != 0u || s >= batch) return;
+    unsigned long long* slot = keys + static_cast<std::size_t>(s) * key_stride + 4u * blockIdx.x;
+    if (wave < 4u) slot[wave] = k;
+    if (wave == 0u)
+      for (std::uint32_t w2 = nw; w2 < 4u; ++w2) slot[w2] = 0ull;  // slots of waves the workgroup lacks
+  }
+};
+
+// Workgroups of mm_kernel<FMT, Epi> of `threads` threads resident per CU (0 if
+// the query fails), cached per size.
+template <int FMT, class Epi>
+int mm_resident(std::uint32_t threads) {
   static int cache[kMaxPanels + 1] = {};
   const std::uint32_t w = threads / 64u;
   if (w == 0u || w > kMaxPanels) return 0;
   if (cache[w] == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mm_kernel<FMT>),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mm_kernel<FMT, Epi>),
                                                      static_cast<int>(threads), 0) != hipSuccess || n <= 0)
       return 0;
     cache[w] = n;
@@ -61,22 +229,13 @@ int mm_resident_fmt(std::uint32_t threads) {
   return cache[w];
 }
 
-inline int mm_resident(int fmt, std::uint32_t threads) {
-  switch (fmt) {
-    case RTXLLM_FMT_IQ2S: return mm_resident_fmt<RTXLLM_FMT_IQ2S>(threads);
-    case RTXLLM_FMT_IQ3S: return mm_resident_fmt<RTXLLM_FMT_IQ3S>(threads);
-    case RTXLLM_FMT_Q5K: return mm_resident_fmt<RTXLLM_FMT_Q5K>(threads);
-    case RTXLLM_FMT_Q4K_RAW: return mm_resident_fmt<RTXLLM_FMT_Q4K_RAW>(threads);
-    case RTXLLM_FMT_Q4K_SPLIT_NATIVE: return mm_resident_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(threads);
-    default: return 0;
-  }
-}
-
 struct MmGeom {
   std::uint32_t ppg, groups, grid;
 };
 
-inline bool mm_geom(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
+// Panel split of a matrix: panels of 512 columns, ppg of them per workgroup
+// (the largest divisor <= 8 of the panel count), groups = panels / ppg.
+inline bool mm_split(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
   if (!fmt_mm_supported(fmt) || rows == 0u || cols == 0u || (cols % kPanel) != 0u) return false;
   const std::uint32_t panels = cols / kPanel;
   g.ppg = 1u;
@@ -86,10 +245,16 @@ inline bool mm_geom(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) 
       break;
     }
   g.groups = panels / g.ppg;
+  return true;
+}
+
+// Persistent grid: the workgroups resident at once, shared by the panel groups,
+// every workgroup taking the same number of tiles (but the last few).
+template <int FMT, class Epi>
+bool mm_geom(std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
+  if (!mm_split(FMT, rows, cols, g)) return false;
   const std::uint32_t tiles = (rows + 15u) / 16u;
-  // persistent: the workgroups resident at once, shared by the panel groups,
-  // every workgroup taking the same number of tiles (but the last few)
-  const int resident = mm_resident(fmt, 64u * g.ppg);
+  const int resident = mm_resident<FMT, Epi>(64u * g.ppg);
   const std::uint32_t per_cu = resident > 0 ? static_cast<std::uint32_t>(resident) : 1u;
   const std::uint32_t cap = std::max(1u, per_cu * static_cast<std::uint32_t>(num_cus()) / g.groups);
   const std::uint32_t rounds = (tiles + cap - 1u) / cap;
@@ -97,27 +262,45 @@ inline bool mm_geom(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) 
   return true;
 }
 
-template <int FMT>
-hipError_t launch_mm_fmt(const QTensor& w, const void* x16, std::uint32_t batch, float* y, float* work,
-                         std::size_t work_bytes, hipStream_t stream) {
+template <int FMT, class Epi>
+hipError_t launch_mm_epi(const QTensor& w, const void* x16, std::uint32_t batch, const Epi& epi, bool one_group,
+                         MmGeom* geom, hipStream_t stream) {
   MmGeom g;
-  if (!mm_geom(FMT, w.rows, w.cols, g)) return hipErrorInvalidValue;
+  if (!mm_geom<FMT, Epi>(w.rows, w.cols, g) || batch == 0u || batch > kBatchMax || x16 == nullptr ||
+      (one_group && g.groups != 1u))
+    return hipErrorInvalidValue;
   const std::uint64_t blocks = static_cast<std::uint64_t>(w.rows) * (w.cols / 256u);
   if (blocks * FmtBytes<FMT>::payload > 0xFFFFFFFFull || blocks * FmtBytes<FMT>::meta > 0xFFFFFFFFull)
     return hipErrorInvalidValue;
-  const std::size_t n = static_cast<std::size_t>(batch) * w.rows;
-  float* out = y;
-  if (g.groups > 1u) {
-    if (work == nullptr || work_bytes < 4u * n * g.groups) return hipErrorInvalidValue;
-    out = work;
-  }
-  hipLaunchKernelGGL(mm_kernel<FMT>, dim3(g.grid, g.groups), dim3(64u * g.ppg), 0, stream, w, x16, batch, out,
-                     w.rows);
-  hipError_t st = hipGetLastError();
-  if (st != hipSuccess || g.groups == 1u) return st;
-  hipLaunchKernelGGL(mm_reduce_kernel, dim3(static_cast<unsigned>((n + 255u) / 256u)), dim3(256), 0, stream, work,
-                     g.groups, static_cast<std::uint32_t>(n), y);
+  if (geom != nullptr) *geom = g;
+  hipLaunchKernelGGL((mm_kernel<FMT, Epi>), dim3(g.grid, g.groups), dim3(64u * g.ppg), 0, stream, w, x16, batch, epi);
   return hipGetLastError();
+}
+
+template <class Epi>
+hipError_t launch_mm(int fmt, const QTensor& w, const void* x16, std::uint32_t batch, const Epi& epi, bool one_group,
+                     MmGeom* geom, hipStream_t stream) {
+  switch (fmt) {
+    case RTXLLM_FMT_IQ2S: return launch_mm_epi<RTXLLM_FMT_IQ2S>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_IQ3S: return launch_mm_epi<RTXLLM_FMT_IQ3S>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_Q5K: return launch_mm_epi<RTXLLM_FMT_Q5K>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_Q4K_RAW: return launch_mm_epi<RTXLLM_FMT_Q4K_RAW>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
+      return launch_mm_epi<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(w, x16, batch, epi, one_group, geom, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <class Epi>
+bool mm_geometry(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
+  switch (fmt) {
+    case RTXLLM_FMT_IQ2S: return mm_geom<RTXLLM_FMT_IQ2S, Epi>(rows, cols, g);
+    case RTXLLM_FMT_IQ3S: return mm_geom<RTXLLM_FMT_IQ3S, Epi>(rows, cols, g);
+    case RTXLLM_FMT_Q5K: return mm_geom<RTXLLM_FMT_Q5K, Epi>(rows, cols, g);
+    case RTXLLM_FMT_Q4K_RAW: return mm_geom<RTXLLM_FMT_Q4K_RAW, Epi>(rows, cols, g);
+    case RTXLLM_FMT_Q4K_SPLIT_NATIVE: return mm_geom<RTXLLM_FMT_Q4K_SPLIT_NATIVE, Epi>(rows, cols, g);
+    default: return false;
+  }
 }
 
 }  // namespace
@@ -125,10 +308,85 @@ hipError_t launch_mm_fmt(const QTensor& w, const void* x16, std::uint32_t batch,
 
 using namespace rtxllm;
 
-extern "C" size_t rtxllm_x16_bytes(uint32_t cols) { return x16_bytes(cols); }
+namespace rtxllm {
 
-extern "C" hipError_t rtxllm_stage_batch(const float* x, uint32_t batch, uint32_t cols, void* x16,
-                                         hipStream_t stream) {
+std::size_t mm_batch_workspace_bytes(int fmt, std::uint32_t rows, std::uint32_t cols) {
+  MmGeom g;
+  if (!mm_split(fmt, rows, cols, g) || g.groups == 1u) return 0u;
+  return 4u * static_cast<std::size_t>(kBatchMax) * rows * g.groups;
+}
+
+std::uint32_t mm_panel_groups(int fmt, std::uint32_t rows, std::uint32_t cols) {
+  MmGeom g;
+  return mm_split(fmt, rows, cols, g) ? g.groups : 0u;
+}
+
+hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                           std::uint32_t cols, const void* x16, std::uint32_t batch, float* out, hipStream_t stream) {
+  if (payload == nullptr || out == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr))
+    return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  return launch_mm(fmt, w, x16, batch, MmStore{out, rows, batch}, false, nullptr, stream);
+}
+
+hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
+                               const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
+                               const float* inv_freq, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                               std::uint32_t table_stride, hipStream_t stream) {
+  if (payload == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) || (q_rows % kHeadDim) != 0u ||
+      (kv_rows % kHeadDim) != 0u || kv.page_size == 0u || table_stride < kv.capacity / kv.page_size)
+    return hipErrorInvalidValue;
+  const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
+  MmQkv e{};
+  e.q_rows = q_rows, e.kv_rows = kv_rows, e.batch = batch, e.table_stride = table_stride;
+  e.inv_freq = inv_freq, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  return launch_mm(fmt, w, x16, batch, e, true, nullptr, stream);
+}
+
+hipError_t launch_mm_gate_up_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta,
+                                   std::uint32_t rows, std::uint32_t cols, const void* x16, std::uint32_t batch,
+                                   float* act, hipStream_t stream) {
+  if (payload == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) || (rows % 2u) != 0u)
+    return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  return launch_mm(fmt, w, x16, batch, MmGateUp{act, rows / 2u}, true, nullptr, stream);
+}
+
+std::uint32_t mm_logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols) {
+  MmGeom g;
+  if (!mm_geometry<MmLogits>(fmt, rows, cols, g)) return 0u;
+  return 4u * g.grid;
+}
+
+hipError_t launch_mm_logits_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                                  std::uint32_t cols, const void* x16, std::uint32_t batch, float* logits,
+                                  unsigned long long* keys, std::uint32_t key_stride, std::uint32_t* key_count,
+                                  hipStream_t stream) {
+  const std::uint32_t slots = mm_logits_key_slots(fmt, rows, cols);
+  if (payload == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) || keys == nullptr ||
+      slots == 0u || slots > key_stride)
+    return hipErrorInvalidValue;
+  if (key_count != nullptr) *key_count = slots;
+  const QTensor w{payload, meta, rows, cols};
+  MmLogits e{};
+  e.logits = logits, e.stride = rows, e.batch = batch, e.keys = keys, e.key_stride = key_stride;
+  return launch_mm(fmt, w, x16, batch, e, true, nullptr, stream);
+}
+
+hipError_t launch_rms_stage_batch(float* h, const float* res, std::uint32_t groups, const std::uint8_t* embed,
+                                  const std::uint32_t* token, std::uint32_t vocab, const float* w, float eps,
+                                  std::uint32_t cols, std::uint32_t batch, void* x16, hipStream_t stream) {
+  if (h == nullptr || x16 == nullptr || cols == 0u || (cols % 256u) != 0u || cols > kStageThreads * kStagePer ||
+      batch == 0u || batch > kBatchMax || (res != nullptr && groups == 0u) ||
+      (embed != nullptr && (token == nullptr || vocab == 0u)))
+    return hipErrorInvalidValue;
+  const RmsStageArgs a{h, res, groups, embed, token, vocab, w, eps, cols, batch, static_cast<_Float16*>(x16)};
+  hipLaunchKernelGGL(rms_stage_batch_kernel, dim3(batch), dim3(kStageThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage_batch(const float* x, std::uint32_t batch, std::uint32_t cols, void* x16,
+                              hipStream_t stream) {
   if (x == nullptr || x16 == nullptr || batch == 0u || batch > kBatchMax || cols == 0u || (cols % 256u) != 0u)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(stage_batch_kernel, dim3(kBatchMax), dim3(1024), 0, stream, x, batch, cols,
@@ -136,28 +394,34 @@ extern "C" hipError_t rtxllm_stage_batch(const float* x, uint32_t batch, uint32_
   return hipGetLastError();
 }
 
+}  // namespace rtxllm
+
+extern "C" size_t rtxllm_x16_bytes(uint32_t cols) { return x16_bytes(cols); }
+
+extern "C" hipError_t rtxllm_stage_batch(const float* x, uint32_t batch, uint32_t cols, void* x16,
+                                         hipStream_t stream) {
+  return launch_stage_batch(x, batch, cols, x16, stream);
+}
+
 extern "C" size_t rtxllm_matvec_batch_workspace(int format, uint32_t rows, uint32_t cols) {
-  MmGeom g;
-  if (!mm_geom(format, rows, cols, g) || g.groups == 1u) return 0u;
-  return 4u * static_cast<std::size_t>(kBatchMax) * rows * g.groups;
+  return mm_batch_workspace_bytes(format, rows, cols);
 }
 
 extern "C" hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
                                           float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
                                           size_t workspace_bytes, hipStream_t stream) {
-  if (payload == nullptr || x16 == nullptr || y == nullptr || batch == 0u || batch > kBatchMax ||
-      ((format == RTXLLM_FMT_Q4K_SPLIT_NATIVE) && meta == nullptr))
-    return hipErrorInvalidValue;
-  const QTensor w{payload, meta, rows, cols};
-  float* work = static_cast<float*>(workspace);
-  switch (format) {
-    case RTXLLM_FMT_IQ2S: return launch_mm_fmt<RTXLLM_FMT_IQ2S>(w, x16, batch, y, work, workspace_bytes, stream);
-    case RTXLLM_FMT_IQ3S: return launch_mm_fmt<RTXLLM_FMT_IQ3S>(w, x16, batch, y, work, workspace_bytes, stream);
-    case RTXLLM_FMT_Q5K: return launch_mm_fmt<RTXLLM_FMT_Q5K>(w, x16, batch, y, work, workspace_bytes, stream);
-    case RTXLLM_FMT_Q4K_RAW:
-      return launch_mm_fmt<RTXLLM_FMT_Q4K_RAW>(w, x16, batch, y, work, workspace_bytes, stream);
-    case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
-      return launch_mm_fmt<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(w, x16, batch, y, work, workspace_bytes, stream);
-    default: return hipErrorInvalidValue;
+  if (y == nullptr || batch == 0u || batch > kBatchMax) return hipErrorInvalidValue;
+  const std::uint32_t groups = mm_panel_groups(format, rows, cols);
+  if (groups == 0u) return hipErrorInvalidValue;
+  const std::size_t n = static_cast<std::size_t>(batch) * rows;
+  float* out = y;
+  if (groups > 1u) {
+    if (workspace == nullptr || workspace_bytes < 4u * n * groups) return hipErrorInvalidValue;
+    out = static_cast<float*>(workspace);
   }
+  hipError_t st = launch_mm_batch(format, payload, meta, rows, cols, x16, batch, out, stream);
+  if (st != hipSuccess || groups == 1u) return st;
+  hipLaunchKernelGGL(mm_reduce_kernel, dim3(static_cast<unsigned>((n + 255u) / 256u)), dim3(256), 0, stream,
+                     static_cast<const float*>(workspace), groups, static_cast<std::uint32_t>(n), y);
+  return hipGetLastError();
 }

@@ -53,7 +53,15 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
 // is also staged (16-value groups) into xq_att for the o projection.
 hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                             std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream);
+// Per sequence partial-record floats (the batch needs batch times as many).
 std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx);
+// The same for `batch` sequences: sequence s has q[s] (n_heads * head_dim
+// floats each), block-table row s (table_stride entries, >= capacity /
+// page_size), position pos[s], and writes att[s]; xq_att must be null when
+// batch > 1 (the batch step stages att with launch_stage_batch).
+hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+                                  std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
+                                  float* partials, float* att, void* xq_att, hipStream_t stream);
 
 // h += W x (rows % 16 == 0), x either the staged input xq_in or the fp32 x_in
 // (staged by each wave itself; exactly one of the two non-null); then xq_next =
@@ -79,6 +87,47 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
 // token[0] = argmax over keys[0, count) (0 if every logit was NaN); *pos += advance.
 hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
                                   std::uint32_t* pos, std::uint32_t advance, hipStream_t stream);
+// The same per sequence s < batch over keys[s * key_stride, + count): token[s], pos[s].
+hipError_t launch_argmax_finalize_batch(const unsigned long long* keys, std::uint32_t key_stride,
+                                        std::uint32_t count, std::uint32_t batch, std::uint32_t* token,
+                                        std::uint32_t* pos, std::uint32_t advance, hipStream_t stream);
+
+// ---- batch (2..8 sequences) step, on the matrix cores (batch.hip) ------------
+// x16: a staged batch activation (rtxllm_x16_bytes); columns of sequences >=
+// batch are never written by these launchers.
+
+// h[s] = embed ? Q5_K row token[s] : h[s] (+ sum over g of res[g][s], res being
+// [groups][batch][cols], when non-null); then x16 = stage(rmsnorm(h[s]) * w).
+hipError_t launch_rms_stage_batch(float* h, const float* res, std::uint32_t groups, const std::uint8_t* embed,
+                                  const std::uint32_t* token, std::uint32_t vocab, const float* w, float eps,
+                                  std::uint32_t cols, std::uint32_t batch, void* x16, hipStream_t stream);
+// x16 = stage(x[s]) for x [batch][cols].
+hipError_t launch_stage_batch(const float* x, std::uint32_t batch, std::uint32_t cols, void* x16,
+                              hipStream_t stream);
+// Panel groups of a batched matvec (1: the output is y itself) and the
+// partial-sum workspace it needs (0 with one group).
+std::uint32_t mm_panel_groups(int fmt, std::uint32_t rows, std::uint32_t cols);
+std::size_t mm_batch_workspace_bytes(int fmt, std::uint32_t rows, std::uint32_t cols);
+// out[g][s][row] = panel group g's part of (W x_s)[row] (out = y with one group).
+hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                           std::uint32_t cols, const void* x16, std::uint32_t batch, float* out, hipStream_t stream);
+// qkv of every sequence with the batch-1 qkv epilogue's RoPE and KV append at
+// pos[s], the KV block table of sequence s being row s (table_stride entries).
+hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
+                               const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
+                               const float* inv_freq, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                               std::uint32_t table_stride, hipStream_t stream);
+// Interleaved gate / up rows: act[s][i] = silu(gate_i) * up_i (act [batch][rows / 2]).
+hipError_t launch_mm_gate_up_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta,
+                                   std::uint32_t rows, std::uint32_t cols, const void* x16, std::uint32_t batch,
+                                   float* act, hipStream_t stream);
+// logits[s][rows] and per sequence mm_logits_key_slots() argmax keys at
+// keys[s * key_stride] (key_stride >= that count), for launch_argmax_finalize_batch.
+std::uint32_t mm_logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols);
+hipError_t launch_mm_logits_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                                  std::uint32_t cols, const void* x16, std::uint32_t batch, float* logits,
+                                  unsigned long long* keys, std::uint32_t key_stride, std::uint32_t* key_count,
+                                  hipStream_t stream);
 
 // Device-side synthetic packs, bit-identical to the host generator
 // (rtxllm_synth_raw_blocks): raw blocks of format 0/5/6/7, or the Q4_K

@@ -15,16 +15,11 @@
 
 #include "dequant.cuh"
 #include "layer.h"
+#include "layer_common.cuh"
 #include "mv_launch.cuh"
 
 namespace rtxllm {
 namespace {
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
 
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
@@ -53,21 +48,6 @@ __device__ __forceinline__ float inv_rms(const float* __restrict__ sumsq, std::u
   }
   s = wave_sum(s);
   return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
-}
-
-__device__ __forceinline__ float silu(float v) {
-  const float sig = 1.0f / (1.0f + expf(-v));
-  return v * sig;
-}
-
-__device__ __forceinline__ std::size_t kv_offset(const KvLayer& kv, std::uint32_t pos, std::uint32_t head) {
-  const std::uint32_t page = static_cast<std::uint32_t>(kv.block_table[pos / kv.page_size]);
-  const std::uint32_t slot = pos % kv.page_size;
-  return ((static_cast<std::size_t>(page) * kv.n_kv + head) * kv.page_size + slot) * kHeadDim;
-}
-
-__device__ __forceinline__ std::uint16_t f2h(float v) {
-  return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
 }
 
 // Stage one 16-value group held by the 16 lanes with owner = true (lane i of
@@ -130,11 +110,11 @@ struct EpiQkv {
         q[row] = out;
       } else {
         const std::uint32_t kr = row - q_rows;
-        kv.k[kv_offset(kv, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
+        kv.k[kv_offset(kv, kv.block_table, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
       }
     } else {
       const std::uint32_t vr = row - q_rows - kv_rows;
-      kv.v[kv_offset(kv, pos, vr / kHeadDim) + (vr & (kHeadDim - 1u))] = f2h(y);
+      kv.v[kv_offset(kv, kv.block_table, pos, vr / kHeadDim) + (vr & (kHeadDim - 1u))] = f2h(y);
     }
   }
 };
@@ -154,14 +134,6 @@ struct EpiGateUp {
     if ((lane & 31u) == 0u && row < rows) act[row >> 1] = silu(y) * up;
   }
 };
-
-__device__ __forceinline__ unsigned long long argmax_key(float v, std::uint32_t row) {
-  if (v != v) return 0ull;           // NaN never wins
-  if (v == 0.0f) v = 0.0f;           // -0 ties with +0 (first index wins)
-  std::uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - row);
-}
 
 // Logits and the greedy argmax: each row group keeps the best key of its tiles
 // in a register and stores it once, after its last tile, into its own slot;
@@ -288,14 +260,25 @@ constexpr std::uint32_t kQPad = kHeadDim / 4u + 1u;    // LDS stride of a quarte
 //    position), p_p taken by readlane;
 //  * the 8 wave records merge in LDS into the chunk's record (m, l, o[128]) per
 //    head: M = max m_w, l = sum e^{m_w - M} l_w, o = sum e^{m_w - M} o_w.
+//
+// Sequence blockIdx.z of a batch: its q, block-table row, position and
+// partial records are q_stride floats, table_stride entries, one word and
+// part_stride floats past those of sequence 0.
 template <int GROUP>
 __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
                                                                        const std::uint32_t* __restrict__ pos_ptr,
                                                                        std::uint32_t nchunks,
-                                                                       float* __restrict__ partials) {
+                                                                       float* __restrict__ partials,
+                                                                       std::uint32_t q_stride,
+                                                                       std::uint32_t table_stride,
+                                                                       std::uint32_t part_stride) {
   __shared__ float qs[GROUP][4][kQPad];
   __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
   const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
+  const std::uint32_t seq = blockIdx.z;
+  q += static_cast<std::size_t>(seq) * q_stride;
+  partials += static_cast<std::size_t>(seq) * part_stride;
+  const std::int32_t* const table = kv.block_table + static_cast<std::size_t>(seq) * table_stride;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::uint32_t p0 = c * kAttnChunk;
   const std::uint32_t wp0 = p0 + kAttnSub * wave;
@@ -305,9 +288,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
   // these loads waits for another.
   const std::uint32_t pc = p0 < kv.capacity ? p0 : kv.capacity - 1u;
   const std::uint32_t pl_pos = wp0 + pl < kv.capacity ? wp0 + pl : kv.capacity - 1u;
-  const std::uint32_t page_c = static_cast<std::uint32_t>(kv.block_table[pc / kv.page_size]);
-  const std::uint32_t page_w = static_cast<std::uint32_t>(kv.block_table[pl_pos / kv.page_size]);
-  const std::uint32_t pos = *pos_ptr < kv.capacity ? *pos_ptr : kv.capacity - 1u;
+  const std::uint32_t page_c = static_cast<std::uint32_t>(table[pc / kv.page_size]);
+  const std::uint32_t page_w = static_cast<std::uint32_t>(table[pl_pos / kv.page_size]);
+  const std::uint32_t pos = pos_ptr[seq] < kv.capacity ? pos_ptr[seq] : kv.capacity - 1u;
   float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * GROUP * (kHeadDim + 2u);
   if (p0 > pos) {  // chunk beyond the context (uniform over the workgroup): empty record
     for (std::uint32_t i = threadIdx.x; i < GROUP * (kHeadDim + 2u); i += blockDim.x)
@@ -420,10 +403,15 @@ constexpr std::uint32_t kCombinePass = 32;  // chunk records per combine pass
 // chunks every load is issued up front: lane c reads chunk c's (m, l) (wave max
 // / sum) and, as lane = dimension pair, the pass's 32 o_c rows; the weights are
 // taken by readlane. Running sums are rescaled when a later pass raises the
-// maximum.
+// maximum. Sequence blockIdx.y of a batch reads its records part_stride floats
+// on and writes att (n_heads * head_dim per sequence) further on; xq (batch 1
+// only) is skipped when null.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
-                                                          std::uint32_t nchunks, float* __restrict__ att, XQOut xq) {
+                                                          std::uint32_t nchunks, float* __restrict__ att, XQOut xq,
+                                                          std::uint32_t part_stride) {
   const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
+  partials += static_cast<std::size_t>(blockIdx.y) * part_stride;
+  att += static_cast<std::size_t>(blockIdx.y) * gridDim.x * kHeadDim;
   const std::uint32_t g = head / group, hh = head % group;
   // every chunk record is merged: chunks past the context hold (-inf, 0, 0),
   // so the kernel needs no position and starts loading at once
@@ -460,6 +448,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const float a0 = o0 / L, a1 = o1 / L;
   const std::uint32_t d0 = head * kHeadDim + 2u * lane;
   *reinterpret_cast<float2*>(att + d0) = make_float2(a0, a1);
+  if (xq.h == nullptr) return;  // the whole grid: a batch stages att separately
   // Stage att for the o projection: the 16-value group of dims [16 k, 16 k + 16)
   // is held by lanes [8 k, 8 k + 8), two values each (the quant16 rule; max and
   // integer sum are order independent, so the digits equal quant16's).
@@ -493,11 +482,16 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   }
 }
 
-// One workgroup of 256: the maximum of count keys, then token and position.
+// One workgroup of 256 per sequence (blockIdx.x, keys key_stride apart): the
+// maximum of count keys, then token and position.
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
                                                               std::uint32_t count, std::uint32_t* token,
-                                                              std::uint32_t* pos, std::uint32_t advance) {
+                                                              std::uint32_t* pos, std::uint32_t advance,
+                                                              std::uint32_t key_stride) {
   __shared__ unsigned long long part[4];
+  keys += static_cast<std::size_t>(blockIdx.x) * key_stride;
+  token += blockIdx.x;
+  if (pos != nullptr) pos += blockIdx.x;
   unsigned long long best = 0ull;
   for (std::uint32_t i0 = threadIdx.x; i0 < count; i0 += 256u * 8u) {
     unsigned long long k[8];
@@ -569,29 +563,46 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
   return static_cast<std::size_t>(n_kv) * nchunks * (n_heads / n_kv) * (kHeadDim + 2u);
 }
 
-hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
+hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+                                  std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
+                                  float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
-      kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u)
+      kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u || batch == 0u ||
+      batch > 65535u || (batch > 1u && (xq_att != nullptr || table_stride < kv.capacity / kv.page_size)))
     return hipErrorInvalidValue;
-  // element offsets of a layer's K / V cache fit 32 bits
-  if (static_cast<std::uint64_t>(kv.capacity) * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  // element offsets of a layer's K / V cache (every sequence's pages) fit 32 bits
+  if (static_cast<std::uint64_t>(kv.capacity) * batch * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const std::uint32_t group = n_heads / kv.n_kv;
   const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
-  const dim3 grid(nchunks, kv.n_kv), block(64 * kAttnWaves);
+  const std::size_t part = attention_partials_floats(n_heads, kv.n_kv, max_ctx);
+  if (part > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  const std::uint32_t part_stride = static_cast<std::uint32_t>(part), q_stride = n_heads * kHeadDim;
+  const dim3 grid(nchunks, kv.n_kv, batch), block(64 * kAttnWaves);
+#define RTXLLM_ATTN_CASE(G)                                                                                      \
+  case G:                                                                                                        \
+    hipLaunchKernelGGL(attn_partial_kernel<G>, grid, block, 0, stream, q, kv, pos, nchunks, partials, q_stride, \
+                       table_stride, part_stride);                                                               \
+    break;
   switch (group) {
-    case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
-    case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
-    case 4: hipLaunchKernelGGL(attn_partial_kernel<4>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
-    case 8: hipLaunchKernelGGL(attn_partial_kernel<8>, grid, block, 0, stream, q, kv, pos, nchunks, partials); break;
+    RTXLLM_ATTN_CASE(1)
+    RTXLLM_ATTN_CASE(2)
+    RTXLLM_ATTN_CASE(4)
+    RTXLLM_ATTN_CASE(8)
     default: return hipErrorInvalidValue;
   }
+#undef RTXLLM_ATTN_CASE
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
-  if (xq_att == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, stream, partials, group, nchunks, att,
-                     xq_out(xq_att, n_heads * kHeadDim));
+  const XQOut xq = xq_att != nullptr ? xq_out(xq_att, n_heads * kHeadDim) : XQOut{};
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads, batch), dim3(64), 0, stream, partials, group, nchunks, att, xq,
+                     part_stride);
   return hipGetLastError();
+}
+
+hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
+  if (xq_att == nullptr) return hipErrorInvalidValue;
+  return launch_attention_batch(q, kv, n_heads, pos, max_ctx, 1u, 0u, partials, att, xq_att, stream);
 }
 
 hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
@@ -633,7 +644,16 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
 
 hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
                                   std::uint32_t* pos, std::uint32_t advance, hipStream_t stream) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, count, token, pos, advance);
+  return launch_argmax_finalize_batch(keys, 0u, count, 1u, token, pos, advance, stream);
+}
+
+hipError_t launch_argmax_finalize_batch(const unsigned long long* keys, std::uint32_t key_stride,
+                                        std::uint32_t count, std::uint32_t batch, std::uint32_t* token,
+                                        std::uint32_t* pos, std::uint32_t advance, hipStream_t stream) {
+  if (keys == nullptr || token == nullptr || batch == 0u || (batch > 1u && key_stride < count))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(batch), dim3(256), 0, stream, keys, count, token, pos, advance,
+                     key_stride);
   return hipGetLastError();
 }
 

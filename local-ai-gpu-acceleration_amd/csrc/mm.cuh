@@ -304,14 +304,27 @@ constexpr int mm_ring() {
   return FMT == RTXLLM_FMT_Q5K ? 2 : (fmt_is_iq(FMT) ? 4 : 3);
 }
 
+// Plain output: out[pg][s][row] (pg = panel group = blockIdx.y, row stride
+// `stride`): y itself with one panel group, else the groups' partial sums.
+struct MmStore {
+  float* out;
+  std::uint32_t stride, batch;
+  __device__ __forceinline__ void init(std::uint32_t) {}
+  __device__ __forceinline__ void operator()(std::uint32_t row, std::uint32_t s, float v, float) const {
+    out[(static_cast<std::size_t>(blockIdx.y) * batch + s) * stride + row] = v;
+  }
+  __device__ __forceinline__ void finish(std::uint32_t, std::uint32_t, std::uint32_t) {}
+};
+
 // Grid: x = workgroups over 16-row tiles (persistent: workgroup g takes tiles
-// g, g + gridDim.x, ...), y = panel group of blockDim.x / 64 panels. Writes
-// out[pg][s][r] (row stride out_stride) for s < batch: y itself with one panel
-// group, else per-group partial sums.
-template <int FMT>
+// g, g + gridDim.x, ...), y = panel group of blockDim.x / 64 panels. Each
+// finished y[s][row] (s < batch) goes to the epilogue: epi.init(s) once per
+// thread (a thread only ever sees one sequence), epi(row, s, y, y of row ^ 1),
+// and epi.finish(wave, lane, waves) after the last tile. Epilogues other than
+// MmStore need a single panel group.
+template <int FMT, class Epi>
 __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const void* __restrict__ x16,
-                                                             std::uint32_t batch, float* __restrict__ out,
-                                                             std::uint32_t out_stride) {
+                                                             std::uint32_t batch, Epi epi) {
   // per-panel partial C of a tile, double buffered by tile parity
   __shared__ float red[2][kMaxPanels][256];
   const std::uint32_t lane = threadIdx.x & 63u;
@@ -338,8 +351,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
   const bool t_store = (t_n & 1u) == 0u && t_s < batch;
   const int t_e = reinterpret_cast<const int*>(xh + 16u * static_cast<std::size_t>(cols))[t_s];
-  float* const t_out = out + static_cast<std::size_t>(blockIdx.y) * batch * out_stride +
-                       static_cast<std::size_t>(t_s) * out_stride;
+  epi.init(t_s);
 
   const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
   const Rsrc rsp = make_rsrc(w.payload, rows * prow);
@@ -366,7 +378,10 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
     const std::uint32_t r = min(r16, rows - 1u - row0);
     mm_load<FMT>(rsp, rsm, r * prow, r * mrow, row0 * prow, row0 * mrow, 2u * panel + (u & 1u), q, raw);
   };
-  if (units == 0u) return;  // whole workgroup: no barrier is left waiting
+  if (units == 0u) {  // whole workgroup: no barrier is left waiting
+    epi.finish(wave, lane, nw);
+    return;
+  }
   constexpr int NB = mm_ring<FMT>();
   MmRaw ring[NB];
 #pragma unroll
@@ -408,8 +423,10 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       float v = 0.0f;
       for (std::uint32_t k = 0; k < nw; ++k) v += red[round & 1u][k][e];
       const float tot = v + __shfl_xor(v, 4, 64);  // column n ^ 1 is lane l ^ 1 = element e ^ 4
+      const float y = ldexpf(tot, t_e);
+      const float partner = __shfl_xor(y, 1, 64);  // row ^ 1 is element e ^ 1
       const std::uint32_t row = (blockIdx.x + round * gridDim.x) * 16u + 4u * (e >> 6) + (e & 3u);
-      if (t_store && row < rows) t_out[row] = ldexpf(tot, t_e);
+      if (t_store && row < rows) epi(row, t_s, y, partner);
     }
   };
 
@@ -430,6 +447,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   static_for<PERIOD>([&](auto jc) {
     if (u0 + decltype(jc)::value < units) step(u0 + decltype(jc)::value, jc);
   });
+  epi.finish(wave, lane, nw);
 }
 
 // y[s][r] = sum over panel groups of partial[pg][s][r].

@@ -1,10 +1,12 @@
-// Llama decode runner (batch 1) on one MI355X: arena layout, synthetic weight
-// fill, the per-step launch sequence and its hipGraph.
+// Llama decode runner (batch 1, or a batch of 2..8 sequences) on one MI355X:
+// arena layout, synthetic weight fill, the per-step launch sequence and its
+// hipGraph.
 //
 // Structure follows the reference's layer-slice runner
 // (runtime/apps/mixed_sequence_benchmark_runner/main.cpp: arena setup
 // 3764-3791, per-stage launches 4002-4279, capture 4801-4823, replay
 // 4825-4836), for a real Llama layer instead of its synthetic stages.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -25,8 +27,10 @@ struct rtxllm_llama {
   rtxllm::VramSuperallocator arena;
   rtxllm::HipGraphBucket graph;
   std::uint32_t q_rows = 0, kv_rows = 0, nslots = 0;
-  std::uint32_t key_slots = 0;  // argmax slots of the LM-head launch
-  std::size_t partial_floats = 0;
+  std::uint32_t key_slots = 0;  // argmax slots of the LM-head launch (per sequence)
+  std::size_t partial_floats = 0;  // attention partial records per sequence
+  std::uint32_t batch = 1, pages_per_seq = 0;
+  std::uint32_t groups_o = 1, groups_down = 1;  // panel groups of the batch o / down matvecs
 };
 
 namespace {
@@ -77,7 +81,7 @@ rtxllm::KvLayer kv_layer(const rtxllm_llama* m, std::uint32_t layer) {
   kv.block_table = region<std::int32_t>(m, layer_name("block_table", layer));
   kv.page_size = m->cfg.page_size;
   kv.n_kv = m->cfg.n_kv_heads;
-  kv.capacity = m->cfg.max_ctx;
+  kv.capacity = m->cfg.max_ctx;  // per sequence
   return kv;
 }
 
@@ -106,6 +110,20 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   if (!shapes_ok || !format_ok(c.fmt_qkv) || !format_ok(c.fmt_o) || !format_ok(c.fmt_gate_up) ||
       !format_ok(c.fmt_down) || !format_ok(c.fmt_lm_head))
     return hipErrorInvalidValue;
+  const std::uint32_t batch = c.batch == 0u ? 1u : c.batch;
+  if (batch > 8u) return hipErrorInvalidValue;
+  if (batch > 1u) {
+    // the batch matvecs take 512-column panels; the fused epilogues (qkv,
+    // gate/up, LM head) need one panel group of at most 8 panels
+    const std::uint32_t q_cols = c.n_heads * rtxllm::kHeadDim;
+    const int mm_fmts[] = {c.fmt_qkv, c.fmt_o, c.fmt_gate_up, c.fmt_down, c.fmt_lm_head};
+    for (int f : mm_fmts)
+      if (f != RTXLLM_FMT_Q4K_RAW && f != RTXLLM_FMT_Q4K_SPLIT_NATIVE && f != RTXLLM_FMT_Q5K &&
+          f != RTXLLM_FMT_IQ2S && f != RTXLLM_FMT_IQ3S)
+        return hipErrorInvalidValue;
+    if (c.hidden % 512u != 0u || c.hidden > 4096u || q_cols % 512u != 0u || c.ffn % 512u != 0u)
+      return hipErrorInvalidValue;
+  }
 
   std::unique_ptr<rtxllm_llama> m(new (std::nothrow) rtxllm_llama());
   if (!m) return hipErrorOutOfMemory;
@@ -114,9 +132,12 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   m->kv_rows = c.n_kv_heads * rtxllm::kHeadDim;
   m->nslots = c.hidden / rtxllm::kXGroup;
   m->partial_floats = rtxllm::attention_partials_floats(c.n_heads, c.n_kv_heads, c.max_ctx);
+  m->batch = batch;
+  m->pages_per_seq = c.max_ctx / c.page_size;
+  const std::size_t B = batch;
 
   const std::size_t kv_halves =
-      static_cast<std::size_t>(c.max_ctx / c.page_size) * c.n_kv_heads * c.page_size * rtxllm::kHeadDim;
+      B * m->pages_per_seq * c.n_kv_heads * c.page_size * rtxllm::kHeadDim;
   std::vector<ArenaSpec> specs;
   for (std::uint32_t l = 0; l < c.n_layers; ++l) {
     add_tensor(specs, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden);
@@ -127,24 +148,34 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     specs.push_back({layer_name("ffn_norm", l), 4u * c.hidden});
     specs.push_back({layer_name("k_cache", l), 2u * kv_halves});
     specs.push_back({layer_name("v_cache", l), 2u * kv_halves});
-    specs.push_back({layer_name("block_table", l), 4u * (c.max_ctx / c.page_size)});
+    specs.push_back({layer_name("block_table", l), 4u * B * m->pages_per_seq});
   }
   specs.push_back({"embed", blocks_of(c.vocab, c.hidden) * 176u});
   add_tensor(specs, "lm_head", c.fmt_lm_head, c.vocab, c.hidden);
   specs.push_back({"out_norm", 4u * c.hidden});
-  specs.push_back({"h", 4u * c.hidden});
+  specs.push_back({"h", 4u * B * c.hidden});
   specs.push_back({"xq", rtxllm::xq_bytes(c.hidden)});
   specs.push_back({"sumsq", 4u * m->nslots});
-  specs.push_back({"q", 4u * m->q_rows});
-  specs.push_back({"att", 4u * m->q_rows});
+  specs.push_back({"q", 4u * B * m->q_rows});
+  specs.push_back({"att", 4u * B * m->q_rows});
   specs.push_back({"xq_att", rtxllm::xq_bytes(m->q_rows)});
-  specs.push_back({"attn_partials", 4u * m->partial_floats});
-  specs.push_back({"act", 4u * c.ffn});
-  specs.push_back({"logits", 4u * c.vocab});
-  m->key_slots = rtxllm::logits_key_slots(c.fmt_lm_head, c.vocab, c.hidden);
-  specs.push_back({"argkeys", 8u * (m->key_slots > 0u ? m->key_slots : 1u)});
-  specs.push_back({"token", 4u});
-  specs.push_back({"pos", 4u});
+  specs.push_back({"attn_partials", 4u * B * m->partial_floats});
+  specs.push_back({"act", 4u * B * c.ffn});
+  specs.push_back({"logits", 4u * B * c.vocab});
+  m->key_slots = batch == 1u ? rtxllm::logits_key_slots(c.fmt_lm_head, c.vocab, c.hidden)
+                             : rtxllm::mm_logits_key_slots(c.fmt_lm_head, c.vocab, c.hidden);
+  if (m->key_slots == 0u) return hipErrorInvalidValue;
+  specs.push_back({"argkeys", 8u * B * m->key_slots});
+  specs.push_back({"token", 4u * B});
+  specs.push_back({"pos", 4u * B});
+  if (batch > 1u) {
+    const std::uint32_t widest = std::max({c.hidden, m->q_rows, c.ffn});
+    specs.push_back({"x16", rtxllm_x16_bytes(widest)});
+    m->groups_o = rtxllm::mm_panel_groups(c.fmt_o, c.hidden, m->q_rows);
+    m->groups_down = rtxllm::mm_panel_groups(c.fmt_down, c.hidden, c.ffn);
+    if (m->groups_o == 0u || m->groups_down == 0u) return hipErrorInvalidValue;
+    specs.push_back({"mm_work", 4u * B * c.hidden * std::max(m->groups_o, m->groups_down)});
+  }
   specs.push_back({"inv_freq", 4u * rtxllm::kHeadDim / 2u});
   try {
     m->arena.initialize(specs);
@@ -160,11 +191,19 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
                                               -2.0 * static_cast<double>(i) / static_cast<double>(rtxllm::kHeadDim)));
   hipError_t st = hipMemcpy(m->arena.arena_ptr("inv_freq"), inv_freq.data(), 4u * inv_freq.size(), hipMemcpyHostToDevice);
   if (st != hipSuccess) return st;
-  std::vector<std::int32_t> table(c.max_ctx / c.page_size);
+  // sequence s owns pages [s * pages_per_seq, (s + 1) * pages_per_seq)
+  std::vector<std::int32_t> table(B * m->pages_per_seq);
   for (std::uint32_t i = 0; i < table.size(); ++i) table[i] = static_cast<std::int32_t>(i);
   for (std::uint32_t l = 0; l < c.n_layers; ++l) {
     st = hipMemcpy(m->arena.arena_ptr(layer_name("block_table", l)), table.data(), 4u * table.size(),
                    hipMemcpyHostToDevice);
+    if (st != hipSuccess) return st;
+  }
+  if (batch > 1u) {  // staged columns of sequences >= batch stay zero
+    std::size_t n = 0;
+    void* x16 = rtxllm_llama_region(m.get(), "x16", 0u, &n);
+    st = hipMemset(x16, 0, n);
+    if (st == hipSuccess) st = hipDeviceSynchronize();
     if (st != hipSuccess) return st;
   }
   *out = m.release();
@@ -227,10 +266,77 @@ namespace {
 
 enum Stage { kEmbed = 0, kQkv = 1, kAttention = 2, kO = 3, kGateUp = 4, kDown = 5, kHead = 6 };
 
+// One stage of layer l for a batch of B > 1 sequences, on the matrix cores:
+// every stage ends with the next matvec's input staged in x16 (residual +
+// RMSNorm fused into the per-sequence staging kernel).
+hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool embed, const float* next_norm,
+                              hipStream_t stream) {
+  const rtxllm_llama_config& c = m->cfg;
+  const std::uint32_t B = m->batch;
+  auto* h = region<float>(m, "h");
+  void* x16 = m->arena.arena_ptr("x16");
+  auto* work = region<float>(m, "mm_work");
+  auto* pos = region<std::uint32_t>(m, "pos");
+  auto* token = region<std::uint32_t>(m, "token");
+  switch (stage) {
+    case kEmbed:
+      return rtxllm::launch_rms_stage_batch(h, nullptr, 0u, embed ? region<std::uint8_t>(m, "embed") : nullptr, token,
+                                            c.vocab, next_norm, c.rms_eps, c.hidden, B, x16, stream);
+    case kQkv: {
+      const TensorRef t = tensor(m, layer_name("qkv", l));
+      return rtxllm::launch_mm_qkv_batch(c.fmt_qkv, t.payload, t.meta, c.hidden, x16, B, m->q_rows, m->kv_rows,
+                                         region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv_layer(m, l),
+                                         m->pages_per_seq, stream);
+    }
+    case kAttention: {
+      hipError_t st = rtxllm::launch_attention_batch(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos,
+                                                     c.max_ctx, B, m->pages_per_seq,
+                                                     region<float>(m, "attn_partials"), region<float>(m, "att"),
+                                                     nullptr, stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_stage_batch(region<float>(m, "att"), B, m->q_rows, x16, stream);
+    }
+    case kO: {
+      const TensorRef t = tensor(m, layer_name("o", l));
+      hipError_t st = rtxllm::launch_mm_batch(c.fmt_o, t.payload, t.meta, c.hidden, m->q_rows, x16, B, work, stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_rms_stage_batch(h, work, m->groups_o, nullptr, nullptr, 0u,
+                                            region<float>(m, layer_name("ffn_norm", l)), c.rms_eps, c.hidden, B, x16,
+                                            stream);
+    }
+    case kGateUp: {
+      const TensorRef t = tensor(m, layer_name("gate_up", l));
+      hipError_t st = rtxllm::launch_mm_gate_up_batch(c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn, c.hidden, x16, B,
+                                                      region<float>(m, "act"), stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_stage_batch(region<float>(m, "act"), B, c.ffn, x16, stream);
+    }
+    case kDown: {
+      const TensorRef t = tensor(m, layer_name("down", l));
+      hipError_t st = rtxllm::launch_mm_batch(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, x16, B, work, stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_rms_stage_batch(h, work, m->groups_down, nullptr, nullptr, 0u, next_norm, c.rms_eps,
+                                            c.hidden, B, x16, stream);
+    }
+    case kHead: {
+      const TensorRef t = tensor(m, "lm_head");
+      auto* keys = region<unsigned long long>(m, "argkeys");
+      std::uint32_t count = 0u;
+      const hipError_t st = rtxllm::launch_mm_logits_batch(c.fmt_lm_head, t.payload, t.meta, c.vocab, c.hidden, x16,
+                                                           B, region<float>(m, "logits"), keys, m->key_slots, &count,
+                                                           stream);
+      if (st != hipSuccess) return st;
+      return rtxllm::launch_argmax_finalize_batch(keys, m->key_slots, count, B, token, pos, 1u, stream);
+    }
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // One stage of layer l; next_norm is the norm weight the down stage stages the
 // residual with (the next layer's attn_norm, or out_norm after the last layer).
 hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed, const float* next_norm,
                         hipStream_t stream) {
+  if (m->batch > 1u) return launch_stage_batch(m, l, stage, embed, next_norm, stream);
   const rtxllm_llama_config& c = m->cfg;
   auto* h = region<float>(m, "h");
   void* xq = m->arena.arena_ptr("xq");
@@ -310,7 +416,9 @@ extern "C" hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream) {
 }
 
 extern "C" uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m) {
-  return m == nullptr ? 0u : 1u + 6u * m->cfg.n_layers + 2u;
+  if (m == nullptr) return 0u;
+  // batch: qkv 1, attention 3 (partials, combine, staging), o / gate-up / down 2 each
+  return m->batch > 1u ? 1u + 10u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
 }
 
 extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream) {

@@ -22,7 +22,9 @@ class LlamaConfig(ctypes.Structure):
                                          "page_size")] + [
         ("rope_theta", c_float),
         ("rms_eps", c_float),
-    ] + [(n, c_int) for n in ("fmt_qkv", "fmt_o", "fmt_gate_up", "fmt_down", "fmt_lm_head")]
+    ] + [(n, c_int) for n in ("fmt_qkv", "fmt_o", "fmt_gate_up", "fmt_down", "fmt_lm_head")] + [
+        ("batch", c_uint32),
+    ]
 
 
 EMBED, HEAD = 1, 2
@@ -46,13 +48,14 @@ class Shape:
     page_size: int = 64
     rope_theta: float = 500000.0
     rms_eps: float = 1e-6
+    batch: int = 1
 
     def config(self, formats: dict | None = None) -> LlamaConfig:
         f = dict(MIXED_8B_FORMATS)
         f.update(formats or {})
         return LlamaConfig(self.hidden, self.n_heads, self.n_kv_heads, self.ffn, self.vocab, self.n_layers,
                            self.max_ctx, self.page_size, self.rope_theta, self.rms_eps, f["fmt_qkv"], f["fmt_o"],
-                           f["fmt_gate_up"], f["fmt_down"], f["fmt_lm_head"])
+                           f["fmt_gate_up"], f["fmt_down"], f["fmt_lm_head"], self.batch)
 
 
 LLAMA_8B = Shape(hidden=4096, n_heads=32, n_kv_heads=8, ffn=14336, vocab=128256, n_layers=32, max_ctx=4096)
@@ -140,6 +143,7 @@ class Llama:
     def launches_per_step(self) -> int:
         return int(lib().rtxllm_llama_launches_per_step(self.h))
 
-    def set_token_pos(self, token: int, pos: int) -> None:
-        self.upload("token", np.array([token], np.uint32))
-        self.upload("pos", np.array([pos], np.uint32))
+    def set_token_pos(self, token, pos) -> None:
+        """token / pos: ints (batch 1) or one per sequence."""
+        self.upload("token", np.atleast_1d(np.asarray(token, np.uint32)))
+        self.upload("pos", np.atleast_1d(np.asarray(pos, np.uint32)))

@@ -74,9 +74,10 @@ class HostModel:
             self.lm_meta = None
         self.out_norm = m.download("out_norm", np.float32)
 
-    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True, layers=None):
+    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True, layers=None, seq: int = 0):
         """Layers (all of this model's, or the given subset) in place on h
-        (float32); returns (h, logits or None)."""
+        (float32) for sequence `seq` (its block-table row and KV pages);
+        returns (h, logits or None)."""
         s, f, P = self.m.shape, self.m.formats, orc.ptr
         lib = orc.lib()
         inv_freq = np.empty(HEAD_DIM // 2, np.float32)
@@ -90,8 +91,9 @@ class HostModel:
                 P(d["wq"]), P(d["wq_meta"]), P(d["wk"]), P(d["wk_meta"]), P(d["wv"]), P(d["wv_meta"]),
                 P(d["o"]), P(d["o_meta"]), P(d["wgate"]), P(d["wgate_meta"]), P(d["wup"]), P(d["wup_meta"]),
                 P(d["down"]), P(d["down_meta"]), P(d["attn_norm"]), P(d["ffn_norm"]))
-            kv = orc.KvCache(P(d["k_cache"]), P(d["v_cache"]), P(d["block_table"]), s.page_size, s.n_kv_heads,
-                             HEAD_DIM)
+            pps = s.max_ctx // s.page_size
+            table = np.ascontiguousarray(d["block_table"][seq * pps:(seq + 1) * pps])
+            kv = orc.KvCache(P(d["k_cache"]), P(d["v_cache"]), P(table), s.page_size, s.n_kv_heads, HEAD_DIM)
             lib.orc_layer_forward(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(kv), pos, P(h), threads)
         if not head:
             return h, None
