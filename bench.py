@@ -7,10 +7,11 @@ down Q4_K split-native, Q5_K embedding and LM head), fp16 paged KV cache of
 hipGraph with the token and position advanced on the device. value = tokens/s.
 
 Also reported: per-stage kernel times of the step (the roofline entry is the
-stage with the largest share of the step), the batch-1 matvec set at the 8B
-FFN shapes (cold weights, GB/s), and the CPU reference path (the oracle's
-scalar restatement of the reference gate) timed on this host on a bounded
-sample.
+stage with the largest share of the step), the same step for a batch of 8
+sequences (one pass over the weights on the matrix cores; tok/s counts all 8),
+the batch-1 matvec set at the 8B FFN shapes (cold weights, GB/s), and the CPU
+reference path (the oracle's scalar restatement of the reference gate) timed
+on this host on a bounded sample.
 
 Prints one JSON line (the driver's contract).
 """
@@ -40,6 +41,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec-set", action="store_true")
+    ap.add_argument("--no-batch8", action="store_true", help="skip the batch-8 decode step")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 256 MiB device copy and each decode stage of layer 0 a few times (for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), print nothing else")
@@ -107,6 +109,9 @@ def layer_weight_bytes(shape) -> dict:
 
 
 def build_model(torch, shape):
+    """The 8B-shape model with its weights, norms and fp16 KV ~ N(0,1); a batch
+    model's sequences share one seeded cache image per layer role (k, v) of
+    all their pages, generated once."""
     import numpy as np
 
     from rtxllm_amd import packs
@@ -117,23 +122,37 @@ def build_model(torch, shape):
     torch.cuda.synchronize()
     H = shape.hidden
     threads = min(16, os.cpu_count() or 1)
+    shared = None
+    if shape.batch > 1:
+        n = m.region_bytes("k_cache", 0) // 2
+        shared = (packs.normal_f16_bits(SEED + 300, n, threads=threads),
+                  packs.normal_f16_bits(SEED + 301, n, threads=threads))
     for l in range(shape.n_layers):
         m.upload("attn_norm", packs.normal_f32(SEED + 100 + 2 * l, H, mean=1.0, std=0.02), layer=l)
         m.upload("ffn_norm", packs.normal_f32(SEED + 101 + 2 * l, H, mean=1.0, std=0.02), layer=l)
-        n = m.region_bytes("k_cache", l) // 2
-        m.upload("k_cache", packs.normal_f16_bits(SEED + 300 + 2 * l, n, threads=threads), layer=l)
-        m.upload("v_cache", packs.normal_f16_bits(SEED + 301 + 2 * l, n, threads=threads), layer=l)
+        if shared is None:
+            n = m.region_bytes("k_cache", l) // 2
+            m.upload("k_cache", packs.normal_f16_bits(SEED + 300 + 2 * l, n, threads=threads), layer=l)
+            m.upload("v_cache", packs.normal_f16_bits(SEED + 301 + 2 * l, n, threads=threads), layer=l)
+        else:
+            m.upload("k_cache", shared[0], layer=l)
+            m.upload("v_cache", shared[1], layer=l)
     m.upload("out_norm", packs.normal_f32(SEED + 99, H, mean=1.0, std=0.02))
-    token = int(np.random.default_rng(SEED).integers(0, shape.vocab))
-    return m, token
+    rng = np.random.default_rng(SEED)
+    tokens = [int(t) for t in rng.integers(0, shape.vocab, size=shape.batch)]
+    return m, (tokens[0] if shape.batch == 1 else tokens)
 
 
-def decode_bench(torch, args) -> dict:
+def decode_bench(torch, args, batch: int = 1) -> dict:
+    """One decode step of `batch` sequences (every one at the same ~4096
+    context) replayed as a hipGraph, plus per-stage kernel times."""
+    import dataclasses
+
     import numpy as np
 
     from rtxllm_amd.llama import LLAMA_8B
 
-    shape = LLAMA_8B
+    shape = dataclasses.replace(LLAMA_8B, batch=batch)
     m, token = build_model(torch, shape)
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
@@ -141,7 +160,7 @@ def decode_bench(torch, args) -> dict:
     if total + 1 > shape.max_ctx:
         raise SystemExit(f"warmup + steps must be < {shape.max_ctx} (KV capacity)")
     pos0 = shape.max_ctx - total - 1  # every timed step attends over ~4096 positions
-    m.set_token_pos(token, pos0)
+    m.set_token_pos(token, [pos0] * batch if batch > 1 else pos0)
     m.graph_capture(sp)
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
@@ -156,18 +175,19 @@ def decode_bench(torch, args) -> dict:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
-    pos_end = int(m.download("pos", np.uint32)[0])
-    assert pos_end == pos0 + total, (pos_end, pos0, total)
-    tokens = [int(m.download("token", np.uint32)[0])]
+    pos_end = m.download("pos", np.uint32)
+    assert all(int(p) == pos0 + total for p in pos_end), (pos_end, pos0, total)
+    tokens = [int(t) for t in m.download("token", np.uint32)]
 
     wb = layer_weight_bytes(shape)
     mean_ctx = pos0 + args.warmup + (args.steps + 1) / 2.0
-    kv_layer = 2 * shape.n_kv_heads * 128 * 2 * mean_ctx
+    kv_layer = batch * 2 * shape.n_kv_heads * 128 * 2 * mean_ctx  # every sequence's K and V
+    # weights once per step, KV, embedding rows and logits per sequence
     step_bytes = shape.n_layers * (wb["qkv"] + wb["o"] + wb["gate_up"] + wb["down"] + kv_layer) + wb["lm_head"] + \
-        (shape.hidden // 256) * 176 + 4 * shape.vocab
+        batch * ((shape.hidden // 256) * 176 + 4 * shape.vocab)
 
     # per-stage kernel time: one graph per stage with one launch per layer
-    m.set_token_pos(token, pos0 + args.warmup)
+    m.set_token_pos(token, [pos0 + args.warmup] * batch if batch > 1 else pos0 + args.warmup)
     stages = {}
     for st in ("qkv", "attention", "o", "gate_up", "down"):
         ms_g = time_graph(torch, stream, lambda st=st: [m.launch_stage(l, st, sp) for l in range(shape.n_layers)])
@@ -187,9 +207,9 @@ def decode_bench(torch, args) -> dict:
     launches = m.launches_per_step()
     m.close()
     return {
-        "ms_per_step": ms, "tok_s": 1e3 / ms, "wall_s": wall, "step_bytes": step_bytes,
+        "ms_per_step": ms, "tok_s": batch * 1e3 / ms, "wall_s": wall, "step_bytes": step_bytes,
         "GB/s": step_bytes / (ms * 1e-3) / 1e9, "stages": stages, "dominant": dom, "launches": launches,
-        "mean_context": mean_ctx, "token_after": tokens[0],
+        "mean_context": mean_ctx, "tokens_after": tokens,
     }
 
 
@@ -404,6 +424,19 @@ def main() -> int:
                      "unit": "GB/s", "frac": dom["frac"], "traffic": traffic_of(dec["dominant"]),
                      "algorithmic_bytes": dom["bytes"], "us_per_launch": dom["us"]},
     }
+    if not args.no_batch8:
+        b8 = decode_bench(torch, args, batch=8)
+        out["batch8"] = {
+            "workload": "the same decode step for 8 sequences at once (one pass over the weights on the matrix "
+                        "cores, every sequence with its own token, position and KV pages, context ~"
+                        f"{int(b8['mean_context'])} each), one hipGraph",
+            "tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 5),
+            "step_hbm_GBps": round(b8["GB/s"], 1), "step_frac_of_hbm_peak": round(b8["GB/s"] / HBM_PEAK_GBS, 4),
+            "step_algorithmic_bytes": int(b8["step_bytes"]), "launches_per_step": b8["launches"],
+            "dtype": "fp16 weight codes x sub-block scale (exact) times hi+lo fp16 activations on the matrix "
+                     "cores, f32 accumulate",
+            "stages": b8["stages"],
+        }
     if not args.no_matvec_set:
         out["matvec_set"] = matvec_set_bench(torch)
     if not args.no_cpu_baseline:

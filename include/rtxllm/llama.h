@@ -60,7 +60,8 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * (int32 [max_ctx / page_size]). Global (layer ignored): "embed", "lm_head",
  * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos",
  * and the work buffers "xq" / "xq_att" (staged activations), "sumsq",
- * "attn_partials", "argkeys", "inv_freq"; with batch > 1 also "x16" (staged
+ * "attn_partials", "argkeys", "inv_freq", "rope" ((cos, sin) of every
+ * position's rotary angles, float2 [max_ctx][64]); with batch > 1 also "x16" (staged
  * batch activation) and "mm_work" (matvec outputs before the residual).
  * With batch B > 1 the per-sequence regions hold B rows, sequence s at row s:
  * h [B][hidden], q / att [B][n_heads*128], act [B][ffn], logits [B][vocab],

@@ -70,7 +70,7 @@ struct RmsStageArgs {
 };
 
 constexpr std::uint32_t kStageThreads = 1024;
-constexpr std::uint32_t kStagePer = 16;  // values per thread: cols <= 16384
+constexpr std::uint32_t kStagePer = 4;  // values per thread: cols <= 4096 (the batch step's hidden size)
 
 __device__ __forceinline__ float block_reduce(float v, float* part, bool is_max) {
 #pragma unroll
@@ -142,8 +142,8 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
 // k (pairs of adjacent rows), q -> q[s], k and v -> the fp16 cache slot of
 // (sequence s, its position); the rule of the batch-1 qkv epilogue.
 struct MmQkv {
-  std::uint32_t q_rows, kv_rows, batch, table_stride;
-  const float* inv_freq;
+  std::uint32_t q_rows, kv_rows, batch, table_stride, rope_positions;
+  const float2* rope;
   const std::uint32_t* pos_ptr;
   float* q;
   KvLayer kv;
@@ -154,9 +154,8 @@ struct MmQkv {
     const std::int32_t* table = kv.block_table + static_cast<std::size_t>(s) * table_stride;
     if (row < q_rows + kv_rows) {
       const std::uint32_t d = row & (kHeadDim - 1u);
-      const float angle = static_cast<float>(pos) * inv_freq[d >> 1];
-      const float sn = sinf(angle), cs = cosf(angle);
-      const float out = (d & 1u) ? (partner * sn + y * cs) : (y * cs - partner * sn);
+      const float2 r = rope_at(rope, rope_positions, pos, d >> 1);
+      const float out = (d & 1u) ? (partner * r.y + y * r.x) : (y * r.x - partner * r.y);
       if (row < q_rows) {
         q[static_cast<std::size_t>(s) * q_rows + row] = out;
       } else {
@@ -331,15 +330,16 @@ hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint
 
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                                const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
-                               const float* inv_freq, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
-                               std::uint32_t table_stride, hipStream_t stream) {
+                               const float2* rope, std::uint32_t rope_positions, const std::uint32_t* pos,
+                               float* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream) {
   if (payload == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) || (q_rows % kHeadDim) != 0u ||
-      (kv_rows % kHeadDim) != 0u || kv.page_size == 0u || table_stride < kv.capacity / kv.page_size)
+      (kv_rows % kHeadDim) != 0u || kv.page_size == 0u || table_stride < kv.capacity / kv.page_size ||
+      rope == nullptr || rope_positions == 0u)
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
   MmQkv e{};
   e.q_rows = q_rows, e.kv_rows = kv_rows, e.batch = batch, e.table_stride = table_stride;
-  e.inv_freq = inv_freq, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  e.rope = rope, e.rope_positions = rope_positions, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
   return launch_mm(fmt, w, x16, batch, e, true, nullptr, stream);
 }
 

@@ -41,12 +41,14 @@ hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::
                             const std::uint32_t* token, float* h, const float* wnorm, void* xq, float* sumsq,
                             std::uint32_t nslots, hipStream_t stream);
 
-// qkv = Wqkv * rmsnorm(h) (q_rows + 2 kv_rows rows, q | k | v), then RoPE (theta
-// schedule inv_freq[head_dim / 2], adjacent pairs) on q and k at position *pos,
-// q -> q_out (fp32), k and v -> fp16 KV cache slot *pos.
+// qkv = Wqkv * rmsnorm(h) (q_rows + 2 kv_rows rows, q | k | v), then RoPE
+// (adjacent pairs) on q and k at position *pos, q -> q_out (fp32), k and v ->
+// fp16 KV cache slot *pos. rope[p * head_dim / 2 + i] = (cos, sin) of the angle
+// of pair i at position p < rope_positions (rope_table()).
 hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
-                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float* inv_freq,
-                      const std::uint32_t* pos, float* q_out, const KvLayer& kv, hipStream_t stream);
+                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
+                      std::uint32_t rope_positions, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                      hipStream_t stream);
 
 // GQA decode attention over positions [0, *pos] of the paged cache: split over
 // context chunks (partials) then combined into att[n_heads * head_dim], which
@@ -115,8 +117,8 @@ hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint
 // pos[s], the KV block table of sequence s being row s (table_stride entries).
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                                const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
-                               const float* inv_freq, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
-                               std::uint32_t table_stride, hipStream_t stream);
+                               const float2* rope, std::uint32_t rope_positions, const std::uint32_t* pos,
+                               float* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream);
 // Interleaved gate / up rows: act[s][i] = silu(gate_i) * up_i (act [batch][rows / 2]).
 hipError_t launch_mm_gate_up_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta,
                                    std::uint32_t rows, std::uint32_t cols, const void* x16, std::uint32_t batch,

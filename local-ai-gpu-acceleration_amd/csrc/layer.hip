@@ -83,8 +83,8 @@ struct EpiQkv {
   const float* sumsq;
   std::uint32_t nslots, n;
   float eps;
-  std::uint32_t q_rows, kv_rows;
-  const float* inv_freq;
+  std::uint32_t q_rows, kv_rows, rope_positions;
+  const float2* rope;
   const std::uint32_t* pos_ptr;
   float* q;
   KvLayer kv;
@@ -102,10 +102,9 @@ struct EpiQkv {
     if (row >= q_rows && pos >= kv.capacity) return;  // no slot for this position
     if (row < q_rows + kv_rows) {
       const std::uint32_t d = row & (kHeadDim - 1u);
-      const float angle = static_cast<float>(pos) * inv_freq[d >> 1];
-      const float s = sinf(angle), c = cosf(angle);
+      const float2 r = rope_at(rope, rope_positions, pos, d >> 1);  // (cos, sin)
       // (e, o) -> (e c - o s, e s + o c)
-      const float out = (d & 1u) ? (partner * s + y * c) : (y * c - partner * s);
+      const float out = (d & 1u) ? (partner * r.y + y * r.x) : (y * r.x - partner * r.y);
       if (row < q_rows) {
         q[row] = out;
       } else {
@@ -549,12 +548,15 @@ hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::
 }
 
 hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
-                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float* inv_freq,
-                      const std::uint32_t* pos, float* q_out, const KvLayer& kv, hipStream_t stream) {
+                      const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
+                      std::uint32_t rope_positions, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                      hipStream_t stream) {
+  if (rope == nullptr || rope_positions == 0u) return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
   EpiQkv e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps;
-  e.q_rows = q_rows, e.kv_rows = kv_rows, e.inv_freq = inv_freq, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  e.q_rows = q_rows, e.kv_rows = kv_rows, e.rope = rope, e.rope_positions = rope_positions;
+  e.pos_ptr = pos, e.q = q_out, e.kv = kv;
   return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, w.rows, e, stream);
 }
 

@@ -29,6 +29,15 @@ __device__ __forceinline__ std::size_t kv_offset(const KvLayer& kv, const std::i
   return ((static_cast<std::size_t>(page) * kv.n_kv + head) * kv.page_size + slot) * kHeadDim;
 }
 
+// (cos, sin) of the rotary angle of pair i at position pos, from the table of
+// positions [0, positions) x kHeadDim / 2 pairs (a position past the table,
+// which has no KV slot either, takes the last row).
+__device__ __forceinline__ float2 rope_at(const float2* rope, std::uint32_t positions, std::uint32_t pos,
+                                          std::uint32_t i) {
+  const std::uint32_t p = pos < positions ? pos : positions - 1u;
+  return rope[static_cast<std::size_t>(p) * (kHeadDim / 2u) + i];
+}
+
 __device__ __forceinline__ std::uint16_t f2h(float v) {
   return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
 }

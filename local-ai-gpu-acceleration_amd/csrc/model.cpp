@@ -177,6 +177,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     specs.push_back({"mm_work", 4u * B * c.hidden * std::max(m->groups_o, m->groups_down)});
   }
   specs.push_back({"inv_freq", 4u * rtxllm::kHeadDim / 2u});
+  specs.push_back({"rope", 8u * static_cast<std::size_t>(c.max_ctx) * (rtxllm::kHeadDim / 2u)});
   try {
     m->arena.initialize(specs);
     m->arena.reset();
@@ -190,6 +191,19 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     inv_freq[i] = static_cast<float>(std::pow(static_cast<double>(c.rope_theta),
                                               -2.0 * static_cast<double>(i) / static_cast<double>(rtxllm::kHeadDim)));
   hipError_t st = hipMemcpy(m->arena.arena_ptr("inv_freq"), inv_freq.data(), 4u * inv_freq.size(), hipMemcpyHostToDevice);
+  if (st != hipSuccess) return st;
+  // rotary table: (cos, sin) of the fp32 angle pos * inv_freq[i] (the product
+  // rounded to fp32, as the textbook RoPE evaluates it), each rounded once
+  // from double, for every position of the cache
+  const std::size_t half = rtxllm::kHeadDim / 2u;
+  std::vector<float> rope(2u * c.max_ctx * half);
+  for (std::uint32_t p = 0; p < c.max_ctx; ++p)
+    for (std::size_t i = 0; i < half; ++i) {
+      const float angle = static_cast<float>(p) * inv_freq[i];
+      rope[2u * (p * half + i)] = static_cast<float>(std::cos(static_cast<double>(angle)));
+      rope[2u * (p * half + i) + 1u] = static_cast<float>(std::sin(static_cast<double>(angle)));
+    }
+  st = hipMemcpy(m->arena.arena_ptr("rope"), rope.data(), 4u * rope.size(), hipMemcpyHostToDevice);
   if (st != hipSuccess) return st;
   // sequence s owns pages [s * pages_per_seq, (s + 1) * pages_per_seq)
   std::vector<std::int32_t> table(B * m->pages_per_seq);
@@ -285,7 +299,7 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
     case kQkv: {
       const TensorRef t = tensor(m, layer_name("qkv", l));
       return rtxllm::launch_mm_qkv_batch(c.fmt_qkv, t.payload, t.meta, c.hidden, x16, B, m->q_rows, m->kv_rows,
-                                         region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv_layer(m, l),
+                                         region<float2>(m, "rope"), c.max_ctx, pos, region<float>(m, "q"), kv_layer(m, l),
                                          m->pages_per_seq, stream);
     }
     case kAttention: {
@@ -350,7 +364,8 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
     case kQkv: {
       const TensorRef t = tensor(m, layer_name("qkv", l));
       return rtxllm::launch_qkv(c.fmt_qkv, t.payload, t.meta, c.hidden, in, m->q_rows, m->kv_rows,
-                                region<float>(m, "inv_freq"), pos, region<float>(m, "q"), kv_layer(m, l), stream);
+                                region<float2>(m, "rope"), c.max_ctx, pos, region<float>(m, "q"), kv_layer(m, l),
+                                stream);
     }
     case kAttention:
       return rtxllm::launch_attention(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
