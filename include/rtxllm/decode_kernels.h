@@ -221,11 +221,15 @@ hipError_t rtxllm_matvec_xq(int format, const uint8_t* payload, const uint8_t* m
  * (the batch-8 decode variant). Formats: 0 Q4_K raw, 4 Q4_K split-native,
  * 5 Q5_K, 6 IQ2_S, 7 IQ3_S; cols % 512 == 0.
  * Staged batch activation ("x16"), rtxllm_x16_bytes(cols) bytes: 16 fp16
- * columns X[n] of cols values, X[2 s] = hi, X[2 s + 1] = lo of x_s 2^-e_s
- * (hi = fp16(x'), lo = fp16(x' - hi), e_s the power of two putting max |x'|
- * in [0.5, 1)), stored in the matrix cores' operand order: the fp16 at
- * ((kb * 8 + j) * 64 + l) * 8 + i is X[l % 16][256 kb + 64 (l / 16) + 8 j + i];
- * then int32 e[8]. The weight codes times their sub-block scale
+ * columns X[n] of cols values, X[2 s] = hi, X[2 s + 1] = lo of x' = x_s
+ * 2^-e[s][b] over each block b of 256 values (hi = fp16(x'), lo = fp16(x' -
+ * hi), e[s][b] the power of two putting the block's max |x'| in [0.5, 1)),
+ * stored in the matrix cores' operand order: the fp16 at ((b * 8 + j) * 64 +
+ * l) * 8 + i is X[l % 16][256 b + 64 (l / 16) + 8 j + i]; then int32
+ * e[8][cols / 256], float ss[8][cols / 256], float eps (rtxllm_stage_batch
+ * writes eps = -1; the decode runner's RMSNorm staging writes eps >= 0 with
+ * the blocks' sums of squares in ss, and the matvec then scales each y[s] by
+ * 1 / sqrt(sum(ss[s]) / cols + eps)). The weight codes times their sub-block scale
  * integers are exact in fp16, so each product is exact and only the ~22-bit
  * hi/lo split and the fp32 accumulation round. Matrices wider than 4096
  * columns need a workspace of rtxllm_matvec_batch_workspace() bytes (0: none). */

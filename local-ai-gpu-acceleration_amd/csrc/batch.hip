@@ -15,47 +15,69 @@
 namespace rtxllm {
 namespace {
 
-// One workgroup per sequence: e_s from max |x_s|, then the hi / lo fp16 pair
-// of x_s 2^-e_s, each at its place in the operand order (x16_index).
-// Sequences >= batch get zero columns.
-__global__ __launch_bounds__(1024) void stage_batch_kernel(const float* __restrict__ x, std::uint32_t batch,
-                                                           std::uint32_t cols, _Float16* __restrict__ x16) {
-  __shared__ float part[16];
-  const std::uint32_t s = blockIdx.x;
-  int* e_out = reinterpret_cast<int*>(x16 + 16u * static_cast<std::size_t>(cols));
-  if (s >= batch) {
-    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
-      const std::size_t i = x16_index(2u * s, c);
-      x16[i] = x16[i + 8u] = static_cast<_Float16>(0.0f);
-    }
-    if (threadIdx.x == 0u) e_out[s] = 0;
-    return;
-  }
-  const float* xs = x + static_cast<std::size_t>(s) * cols;
-  float m = 0.0f;
-  for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) m = fmaxf(m, fabsf(xs[c]));
+// ---- staging: one workgroup of 256 per (block b of 256 values, sequence s) ----
+
+constexpr std::uint32_t kStageThreads = 256;
+
+// Sum (is_max false) or maximum over the 256 threads; every thread gets it.
+__device__ __forceinline__ float block_reduce(float v, float* part, bool is_max) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = m;
-  __syncthreads();
-  m = 0.0f;
-  for (std::uint32_t i = 0; i < blockDim.x / 64u; ++i) m = fmaxf(m, part[i]);
-  int e = 0;
-  if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
-  for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
-    const float v = ldexpf(xs[c], -e);
-    const _Float16 h = static_cast<_Float16>(v);
-    const std::size_t i = x16_index(2u * s, c);
-    x16[i] = h;
-    x16[i + 8u] = static_cast<_Float16>(v - static_cast<float>(h));  // column 2 s + 1: lane + 1
+  for (int o = 32; o > 0; o >>= 1) {
+    const float t = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, t) : v + t;
   }
-  if (threadIdx.x == 0u) e_out[s] = e;
+  __syncthreads();  // part may still be read by a previous reduction
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r0 = part[0], r1 = part[1], r2 = part[2], r3 = part[3];
+  return is_max ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (r0 + r1) + (r2 + r3);
 }
 
-// Residual + RMSNorm + staging of one batch step, one workgroup per sequence
-// s < batch: v = embed ? dequant(embed[token[s]]) : h[s] (+ the panel groups'
-// partial sums res[g][s] in group order, when res is set); h[s] = v; then x16
-// columns of s = stage(v / sqrt(mean(v^2) + eps) * w).
+// x (already normalised or plain) of thread c of block b, sequence s: e[s][b]
+// from the block's max |x|, then the hi / lo fp16 pair of x 2^-e at its place
+// in the operand order.
+__device__ __forceinline__ void stage_block_value(float x, std::uint32_t s, std::uint32_t b, std::uint32_t c,
+                                                  std::uint32_t cols, _Float16* x16, float* part) {
+  const float m = block_reduce(fabsf(x), part, true);
+  int e = 0;
+  if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+  const float v = ldexpf(x, -e);
+  const _Float16 hi = static_cast<_Float16>(v);
+  const std::size_t i = x16_index(2u * s, c);
+  x16[i] = hi;
+  x16[i + 8u] = static_cast<_Float16>(v - static_cast<float>(hi));  // column 2 s + 1: lane + 1
+  if (threadIdx.x == 0u) x16_tail(x16, cols).e[s * (cols / 256u) + b] = e;
+}
+
+// Sequences >= batch: zero columns, exponent 0, sum of squares 0.
+__device__ __forceinline__ void stage_block_zero(std::uint32_t s, std::uint32_t b, std::uint32_t c,
+                                                 std::uint32_t cols, _Float16* x16) {
+  const std::size_t i = x16_index(2u * s, c);
+  x16[i] = x16[i + 8u] = static_cast<_Float16>(0.0f);
+  if (threadIdx.x == 0u) {
+    const X16Tail t = x16_tail(x16, cols);
+    t.e[s * (cols / 256u) + b] = 0;
+    t.ss[s * (cols / 256u) + b] = 0.0f;
+  }
+}
+
+// Plain staging of x [batch][cols]; grid (cols / 256, 8).
+__global__ __launch_bounds__(kStageThreads) void stage_batch_kernel(const float* __restrict__ x, std::uint32_t batch,
+                                                                    std::uint32_t cols, _Float16* __restrict__ x16) {
+  __shared__ float part[kStageThreads / 64u];
+  const std::uint32_t b = blockIdx.x, s = blockIdx.y, c = 256u * b + threadIdx.x;
+  if (b == 0u && s == 0u && threadIdx.x == 0u) *x16_tail(x16, cols).eps = -1.0f;
+  if (s >= batch) {
+    stage_block_zero(s, b, c, cols, x16);
+    return;
+  }
+  stage_block_value(x[static_cast<std::size_t>(s) * cols + c], s, b, c, cols, x16, part);
+}
+
+// Residual + RMSNorm staging of one batch step: v = embed ? dequant(embed
+// [token[s]]) : h[s] (+ the panel groups' partial sums res[g][s] in group
+// order, when res is set); h[s] = v; x16 = rmsnorm-staged v * w (the block's
+// sum of v^2 in ss, the 1 / rms left to the consumer).
 struct RmsStageArgs {
   float* h;              // [batch][cols]
   const float* res;      // [groups][batch][cols] or null
@@ -69,71 +91,29 @@ struct RmsStageArgs {
   _Float16* x16;
 };
 
-constexpr std::uint32_t kStageThreads = 1024;
-constexpr std::uint32_t kStagePer = 4;  // values per thread: cols <= 4096 (the batch step's hidden size)
-
-__device__ __forceinline__ float block_reduce(float v, float* part, bool is_max) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float t = __shfl_xor(v, o, 64);
-    v = is_max ? fmaxf(v, t) : v + t;
-  }
-  __syncthreads();  // part may still be read by a previous reduction
-  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float r = part[0];
-  for (std::uint32_t i = 1; i < blockDim.x / 64u; ++i) r = is_max ? fmaxf(r, part[i]) : r + part[i];
-  return r;
-}
-
 __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStageArgs a) {
   __shared__ float part[kStageThreads / 64u];
-  const std::uint32_t s = blockIdx.x, cols = a.cols;
+  const std::uint32_t b = blockIdx.x, s = blockIdx.y, c = 256u * b + threadIdx.x, cols = a.cols;
+  if (b == 0u && s == 0u && threadIdx.x == 0u) *x16_tail(a.x16, cols).eps = a.eps;
+  if (s >= a.batch) {
+    stage_block_zero(s, b, c, cols, a.x16);
+    return;
+  }
   float* const hs = a.h + static_cast<std::size_t>(s) * cols;
-  const std::uint8_t* erow = nullptr;
+  float x;
   if (a.embed != nullptr) {
     const std::uint32_t tok = a.token[s] < a.vocab ? a.token[s] : a.vocab - 1u;
-    erow = a.embed + static_cast<std::size_t>(tok) * (cols / 256u) * 176u;
+    const std::uint8_t* blk = a.embed + (static_cast<std::size_t>(tok) * (cols / 256u) + b) * 176u;
+    x = dequant_value<RTXLLM_FMT_Q5K>(blk, nullptr, threadIdx.x);
+  } else {
+    x = hs[c];
   }
-  float v[kStagePer];
-  float sq = 0.0f;
-#pragma unroll
-  for (std::uint32_t k = 0; k < kStagePer; ++k) {
-    const std::uint32_t c = threadIdx.x + kStageThreads * k;
-    v[k] = 0.0f;
-    if (c >= cols) continue;
-    float x = erow != nullptr ? dequant_value<RTXLLM_FMT_Q5K>(erow + (c / 256u) * 176u, nullptr, c & 255u) : hs[c];
-    if (a.res != nullptr)
-      for (std::uint32_t g = 0; g < a.groups; ++g)
-        x += a.res[(static_cast<std::size_t>(g) * a.batch + s) * cols + c];
-    if (erow != nullptr || a.res != nullptr) hs[c] = x;
-    v[k] = x;
-    sq += x * x;
-  }
-  sq = block_reduce(sq, part, false);
-  const float inv = 1.0f / sqrtf(sq / static_cast<float>(cols) + a.eps);
-  float m = 0.0f;
-#pragma unroll
-  for (std::uint32_t k = 0; k < kStagePer; ++k) {
-    const std::uint32_t c = threadIdx.x + kStageThreads * k;
-    if (c >= cols) continue;
-    v[k] = a.w != nullptr ? v[k] * inv * a.w[c] : v[k] * inv;
-    m = fmaxf(m, fabsf(v[k]));
-  }
-  m = block_reduce(m, part, true);
-  int e = 0;
-  if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);
-#pragma unroll
-  for (std::uint32_t k = 0; k < kStagePer; ++k) {
-    const std::uint32_t c = threadIdx.x + kStageThreads * k;
-    if (c >= cols) continue;
-    const float x = ldexpf(v[k], -e);
-    const _Float16 hi = static_cast<_Float16>(x);
-    const std::size_t i = x16_index(2u * s, c);
-    a.x16[i] = hi;
-    a.x16[i + 8u] = static_cast<_Float16>(x - static_cast<float>(hi));
-  }
-  if (threadIdx.x == 0u) reinterpret_cast<int*>(a.x16 + 16u * static_cast<std::size_t>(cols))[s] = e;
+  if (a.res != nullptr)
+    for (std::uint32_t g = 0; g < a.groups; ++g) x += a.res[(static_cast<std::size_t>(g) * a.batch + s) * cols + c];
+  if (a.embed != nullptr || a.res != nullptr) hs[c] = x;
+  const float ss = block_reduce(x * x, part, false);
+  if (threadIdx.x == 0u) x16_tail(a.x16, cols).ss[s * (cols / 256u) + b] = ss;
+  stage_block_value(a.w != nullptr ? x * a.w[c] : x, s, b, c, cols, a.x16, part);
 }
 
 // ---- batch epilogues --------------------------------------------------------
@@ -376,12 +356,11 @@ hipError_t launch_mm_logits_batch(int fmt, const std::uint8_t* payload, const st
 hipError_t launch_rms_stage_batch(float* h, const float* res, std::uint32_t groups, const std::uint8_t* embed,
                                   const std::uint32_t* token, std::uint32_t vocab, const float* w, float eps,
                                   std::uint32_t cols, std::uint32_t batch, void* x16, hipStream_t stream) {
-  if (h == nullptr || x16 == nullptr || cols == 0u || (cols % 256u) != 0u || cols > kStageThreads * kStagePer ||
-      batch == 0u || batch > kBatchMax || (res != nullptr && groups == 0u) ||
-      (embed != nullptr && (token == nullptr || vocab == 0u)))
+  if (h == nullptr || x16 == nullptr || cols == 0u || (cols % 256u) != 0u || batch == 0u || batch > kBatchMax ||
+      (res != nullptr && groups == 0u) || (embed != nullptr && (token == nullptr || vocab == 0u)) || !(eps >= 0.0f))
     return hipErrorInvalidValue;
   const RmsStageArgs a{h, res, groups, embed, token, vocab, w, eps, cols, batch, static_cast<_Float16*>(x16)};
-  hipLaunchKernelGGL(rms_stage_batch_kernel, dim3(batch), dim3(kStageThreads), 0, stream, a);
+  hipLaunchKernelGGL(rms_stage_batch_kernel, dim3(cols / 256u, kBatchMax), dim3(kStageThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -389,7 +368,7 @@ hipError_t launch_stage_batch(const float* x, std::uint32_t batch, std::uint32_t
                               hipStream_t stream) {
   if (x == nullptr || x16 == nullptr || batch == 0u || batch > kBatchMax || cols == 0u || (cols % 256u) != 0u)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(stage_batch_kernel, dim3(kBatchMax), dim3(1024), 0, stream, x, batch, cols,
+  hipLaunchKernelGGL(stage_batch_kernel, dim3(cols / 256u, kBatchMax), dim3(kStageThreads), 0, stream, x, batch, cols,
                      static_cast<_Float16*>(x16));
   return hipGetLastError();
 }

@@ -41,10 +41,26 @@ constexpr std::uint32_t kBatchMax = 8;
 constexpr std::uint32_t kPanel = 512;        // columns per wave
 constexpr std::uint32_t kMaxPanels = 8;      // waves per workgroup
 
-// Staged batch activation: 16 fp16 columns X[n] (n = 2 s + hi/lo) of cols
-// values in operand order (x16_index), then int32 e[8].
+// Staged batch activation of cols values per sequence (cols % 256 == 0,
+// nb = cols / 256 blocks): 16 fp16 columns X[n] (n = 2 s + hi/lo) in operand
+// order (x16_index), holding x_s 2^-e[s][b] over block b; then int32
+// e[8][nb]; float ss[8][nb]; float eps. With eps >= 0 the vector is
+// rmsnorm-staged: its consumer scales W x by 1 / sqrt(sum_b ss[s][b] / cols +
+// eps) (ss = the sequence's sums of squares per block); eps < 0: no scale.
 __host__ __device__ inline std::size_t x16_bytes(std::uint32_t cols) {
-  return 32u * static_cast<std::size_t>(cols) + 4u * kBatchMax;
+  return 32u * static_cast<std::size_t>(cols) + 8u * kBatchMax * (cols / 256u) + 16u;
+}
+
+struct X16Tail {
+  int* e;       // [8][nb]
+  float* ss;    // [8][nb]
+  float* eps;
+};
+
+__host__ __device__ inline X16Tail x16_tail(const void* x16, std::uint32_t cols) {
+  auto* base = static_cast<std::uint8_t*>(const_cast<void*>(x16)) + 32u * static_cast<std::size_t>(cols);
+  const std::size_t n = static_cast<std::size_t>(kBatchMax) * (cols / 256u);
+  return {reinterpret_cast<int*>(base), reinterpret_cast<float*>(base + 4u * n), reinterpret_cast<float*>(base + 8u * n)};
 }
 
 // Index (in fp16 values) of X[n][c]: the place where lane l = 16 (k / 64) + n
@@ -336,7 +352,6 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t tiles = (rows + 15u) >> 4;
 
   // B operands of the panel: 2 blocks x 8 instructions, 1 KB of whole lanes each.
-  const _Float16* xh = static_cast<const _Float16*>(x16);
   const uint4* xb = reinterpret_cast<const uint4*>(x16) + 2u * panel * 8u * 64u + lane;
   uint4 B[2][8];
 #pragma unroll
@@ -344,13 +359,27 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
 #pragma unroll
     for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
 
+  // The lane's C column is n = lane % 16 = 2 s + hi/lo: its products of block
+  // b of the panel carry that sequence's block exponent, 2^e[s][b].
+  const X16Tail tail = x16_tail(x16, cols);
+  const std::uint32_t nb = cols >> 8;
+  float fb[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + 2u * panel + b]);
+
   // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
   // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
   // n = l % 16 = 2 s + hi/lo. blockDim.x being a multiple of 64, n and s are
-  // the same for all of a thread's elements.
+  // the same for all of a thread's elements; t_post is the sequence's RMSNorm
+  // scale (1 for a plainly staged input).
   const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
   const bool t_store = (t_n & 1u) == 0u && t_s < batch;
-  const int t_e = reinterpret_cast<const int*>(xh + 16u * static_cast<std::size_t>(cols))[t_s];
+  float t_post = 1.0f;
+  if (*tail.eps >= 0.0f) {
+    float ss = 0.0f;
+    for (std::uint32_t b = 0; b < nb; ++b) ss += tail.ss[t_s * nb + b];
+    t_post = 1.0f / sqrtf(ss / static_cast<float>(cols) + *tail.eps);
+  }
   epi.init(t_s);
 
   const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
@@ -400,15 +429,16 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       if constexpr (!fmt_is_iq(FMT)) cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, as_half8(B[b][j]), cm, 0, 0, 0);
     }
     // the C rows of this lane are 4 (l / 16) + i; their scales live in the
-    // lanes that loaded those rows (lane = row, q = 0)
+    // lanes that loaded those rows (lane = row, q = 0); the block exponent of
+    // the lane's column is a power of two (exact)
     float d, dmin;
     mm_block_scale<FMT>(raw, d, dmin);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int src = static_cast<int>(4u * q) + i;
-      const float di = __shfl(d, src, 64);
+      const float di = __shfl(d, src, 64) * fb[b];
       acc[i] = __builtin_fmaf(c[i], di, acc[i]);
-      if constexpr (!fmt_is_iq(FMT)) acc[i] = __builtin_fmaf(-cm[i], __shfl(dmin, src, 64), acc[i]);
+      if constexpr (!fmt_is_iq(FMT)) acc[i] = __builtin_fmaf(-cm[i], __shfl(dmin, src, 64) * fb[b], acc[i]);
     }
   };
   // tile done: every panel's partial to LDS, one barrier, then each of the 256
@@ -423,7 +453,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       float v = 0.0f;
       for (std::uint32_t k = 0; k < nw; ++k) v += red[round & 1u][k][e];
       const float tot = v + __shfl_xor(v, 4, 64);  // column n ^ 1 is lane l ^ 1 = element e ^ 4
-      const float y = ldexpf(tot, t_e);
+      const float y = tot * t_post;
       const float partner = __shfl_xor(y, 1, 64);  // row ^ 1 is element e ^ 1
       const std::uint32_t row = (blockIdx.x + round * gridDim.x) * 16u + 4u * (e >> 6) + (e & 3u);
       if (t_store && row < rows) epi(row, t_s, y, partner);
