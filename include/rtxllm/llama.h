@@ -63,8 +63,10 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * "attn_partials", "argkeys", "inv_freq", "rope" ((cos, sin) of every
  * position's rotary angles, float2 [max_ctx][64]); with batch > 1 also "x16" (staged
  * batch activation) and "mm_work" (matvec outputs before the residual).
+ * "q" holds the rotated query as the attention's operand: per sequence and kv
+ * head 4096 bytes of fp16 hi / lo pairs of q / sqrt(128) (matrix-core order).
  * With batch B > 1 the per-sequence regions hold B rows, sequence s at row s:
- * h [B][hidden], q / att [B][n_heads*128], act [B][ffn], logits [B][vocab],
+ * h [B][hidden], q, att [B][n_heads*128], act [B][ffn], logits [B][vocab],
  * token / pos [B]; the KV caches hold B * max_ctx / page_size pages and
  * block_table is [B][max_ctx / page_size] (initially sequence s owns pages
  * [s * max_ctx / page_size, (s + 1) * max_ctx / page_size)).

@@ -122,10 +122,10 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
 // k (pairs of adjacent rows), q -> q[s], k and v -> the fp16 cache slot of
 // (sequence s, its position); the rule of the batch-1 qkv epilogue.
 struct MmQkv {
-  std::uint32_t q_rows, kv_rows, batch, table_stride, rope_positions;
+  std::uint32_t q_rows, kv_rows, batch, table_stride, rope_positions, group;
   const float2* rope;
   const std::uint32_t* pos_ptr;
-  float* q;
+  _Float16* q;  // q16 of sequence 0; sequence s kv.n_kv * kQ16PerKv values on
   KvLayer kv;
   std::uint32_t pos;
   __device__ __forceinline__ void init(std::uint32_t s) { pos = s < batch ? pos_ptr[s] : 0u; }
@@ -137,7 +137,7 @@ struct MmQkv {
       const float2 r = rope_at(rope, rope_positions, pos, d >> 1);
       const float out = (d & 1u) ? (partner * r.y + y * r.x) : (y * r.x - partner * r.y);
       if (row < q_rows) {
-        q[static_cast<std::size_t>(s) * q_rows + row] = out;
+        q16_store(q + static_cast<std::size_t>(s) * kv.n_kv * kQ16PerKv, row / kHeadDim, group, d, out);
       } else {
         const std::uint32_t kr = row - q_rows;
         kv.k[kv_offset(kv, table, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
@@ -311,15 +311,16 @@ hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                                const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
                                const float2* rope, std::uint32_t rope_positions, const std::uint32_t* pos,
-                               float* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream) {
+                               void* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream) {
   if (payload == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) || (q_rows % kHeadDim) != 0u ||
       (kv_rows % kHeadDim) != 0u || kv.page_size == 0u || table_stride < kv.capacity / kv.page_size ||
-      rope == nullptr || rope_positions == 0u)
+      rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || q_rows % (kHeadDim * kv.n_kv) != 0u)
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
   MmQkv e{};
   e.q_rows = q_rows, e.kv_rows = kv_rows, e.batch = batch, e.table_stride = table_stride;
-  e.rope = rope, e.rope_positions = rope_positions, e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  e.rope = rope, e.rope_positions = rope_positions, e.pos_ptr = pos, e.q = static_cast<_Float16*>(q_out), e.kv = kv;
+  e.group = q_rows / kHeadDim / kv.n_kv;
   return launch_mm(fmt, w, x16, batch, e, true, nullptr, stream);
 }
 

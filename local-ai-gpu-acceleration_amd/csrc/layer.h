@@ -33,6 +33,11 @@ struct NormIn {
 };
 
 constexpr std::uint32_t kHeadDim = 128;
+// The attention's query operand ("q16"): per sequence and kv head, the rotated
+// query heads of the kv head scaled by 1 / sqrt(head_dim) as fp16 hi / lo
+// pairs in matrix-core operand order, kQ16BytesPerKv bytes (zero where a kv
+// head has fewer than 8 query heads; the qkv launchers never write there).
+constexpr std::uint32_t kQ16BytesPerKv = 4096;
 
 // h = dequant(embed[*token]) (Q5_K row, bit-exact; table null: h as is), then
 // xq = stage(h * wnorm), sumsq[0] = sum(h^2), sumsq[1, nslots) = 0.
@@ -42,26 +47,26 @@ hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::
                             std::uint32_t nslots, hipStream_t stream);
 
 // qkv = Wqkv * rmsnorm(h) (q_rows + 2 kv_rows rows, q | k | v), then RoPE
-// (adjacent pairs) on q and k at position *pos, q -> q_out (fp32), k and v ->
+// (adjacent pairs) on q and k at position *pos, q -> q_out (q16), k and v ->
 // fp16 KV cache slot *pos. rope[p * head_dim / 2 + i] = (cos, sin) of the angle
 // of pair i at position p < rope_positions (rope_table()).
 hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                       const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
-                      std::uint32_t rope_positions, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                      std::uint32_t rope_positions, const std::uint32_t* pos, void* q_out, const KvLayer& kv,
                       hipStream_t stream);
 
 // GQA decode attention over positions [0, *pos] of the paged cache: split over
 // context chunks (partials) then combined into att[n_heads * head_dim], which
 // is also staged (16-value groups) into xq_att for the o projection.
-hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+hipError_t launch_attention(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                             std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream);
 // Per sequence partial-record floats (the batch needs batch times as many).
 std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx);
-// The same for `batch` sequences: sequence s has q[s] (n_heads * head_dim
-// floats each), block-table row s (table_stride entries, >= capacity /
+// The same for `batch` sequences: sequence s has q16 n_kv * kQ16BytesPerKv
+// bytes on, block-table row s (table_stride entries, >= capacity /
 // page_size), position pos[s], and writes att[s]; xq_att must be null when
 // batch > 1 (the batch step stages att with launch_stage_batch).
-hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                                   std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
                                   float* partials, float* att, void* xq_att, hipStream_t stream);
 
@@ -118,7 +123,7 @@ hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                                const void* x16, std::uint32_t batch, std::uint32_t q_rows, std::uint32_t kv_rows,
                                const float2* rope, std::uint32_t rope_positions, const std::uint32_t* pos,
-                               float* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream);
+                               void* q_out, const KvLayer& kv, std::uint32_t table_stride, hipStream_t stream);
 // Interleaved gate / up rows: act[s][i] = silu(gate_i) * up_i (act [batch][rows / 2]).
 hipError_t launch_mm_gate_up_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta,
                                    std::uint32_t rows, std::uint32_t cols, const void* x16, std::uint32_t batch,

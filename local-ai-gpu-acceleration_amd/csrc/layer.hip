@@ -83,10 +83,10 @@ struct EpiQkv {
   const float* sumsq;
   std::uint32_t nslots, n;
   float eps;
-  std::uint32_t q_rows, kv_rows, rope_positions;
+  std::uint32_t q_rows, kv_rows, rope_positions, group;
   const float2* rope;
   const std::uint32_t* pos_ptr;
-  float* q;
+  _Float16* q;  // q16 operand order
   KvLayer kv;
   float scale;
   std::uint32_t pos;
@@ -106,7 +106,7 @@ struct EpiQkv {
       // (e, o) -> (e c - o s, e s + o c)
       const float out = (d & 1u) ? (partner * r.y + y * r.x) : (y * r.x - partner * r.y);
       if (row < q_rows) {
-        q[row] = out;
+        q16_store(q, row / kHeadDim, group, d, out);
       } else {
         const std::uint32_t kr = row - q_rows;
         kv.k[kv_offset(kv, kv.block_table, pos, kr / kHeadDim) + (kr & (kHeadDim - 1u))] = f2h(out);
@@ -245,16 +245,20 @@ constexpr std::uint32_t kAttnWaves = 8;                // waves per workgroup
 constexpr std::uint32_t kAttnSub = 16;                 // positions per wave
 constexpr std::uint32_t kAttnChunk = kAttnWaves * kAttnSub;  // positions per workgroup
 constexpr std::uint32_t kMaxGroup = 8;
-constexpr std::uint32_t kQPad = kHeadDim / 4u + 1u;    // LDS stride of a quarter of q (bank spread)
 
 // One workgroup of 8 waves per (chunk c of 128 positions, kv head g): the
 // `GROUP` query heads of g over positions [128 c, 128 c + 128) ∩ [0, pos]. Wave
 // w takes positions [128 c + 16 w, +16); all its K and V loads are issued up
 // front. Then:
-//  * scores: lane = (position 0..15, quarter of the head dims); the lane dots
-//    its 32 dims of the K row with the heads' q (from LDS, broadcast within a
-//    quarter) and two xor-shuffles sum the quarters;
-//  * wave softmax per head: m = max, p = exp(s - m), l = sum p;
+//  * scores on the matrix cores: S = K q^T for the 16 positions and every head
+//    at once, four v_mfma_f32_16x16x32_f16 over the 128 dims. A = the K rows
+//    (lane = (position r = l % 16, dims [32 (l / 16), +32)), fp16 as stored);
+//    B = q / sqrt(128) of head n / 2 as an fp16 hi (n even) / lo (n odd) pair,
+//    column n of 16 (columns >= 2 GROUP zero), so every product is exact and
+//    the pair carries ~22 bits of q; C[position][n] summed over the pair;
+//  * softmax of every head at once: the lanes of column 2 h hold head h's
+//    scores for positions 4 (l / 16) + i, i < 4: max and sum over i and two
+//    xor-shuffles;
 //  * o = sum_p p_p v_p: lane = dimension pair, V rows coalesced (256 B per
 //    position), p_p taken by readlane;
 //  * the 8 wave records merge in LDS into the chunk's record (m, l, o[128]) per
@@ -264,14 +268,15 @@ constexpr std::uint32_t kQPad = kHeadDim / 4u + 1u;    // LDS stride of a quarte
 // partial records are q_stride floats, table_stride entries, one word and
 // part_stride floats past those of sequence 0.
 template <int GROUP>
-__global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const float* __restrict__ q, KvLayer kv,
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Float16* __restrict__ q, KvLayer kv,
                                                                        const std::uint32_t* __restrict__ pos_ptr,
                                                                        std::uint32_t nchunks,
                                                                        float* __restrict__ partials,
                                                                        std::uint32_t q_stride,
                                                                        std::uint32_t table_stride,
                                                                        std::uint32_t part_stride) {
-  __shared__ float qs[GROUP][4][kQPad];
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
   const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
   const std::uint32_t seq = blockIdx.z;
@@ -281,14 +286,14 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::uint32_t p0 = c * kAttnChunk;
   const std::uint32_t wp0 = p0 + kAttnSub * wave;
-  const std::uint32_t pl = lane >> 2, qd = lane & 3u;
+  const std::uint32_t r = lane & 15u, qq = lane >> 4;
   // The lane's position and the chunk's first position, clamped into the
-  // cache, and their block-table entries are read together with *pos: none of
-  // these loads waits for another.
+  // cache, and their block-table entries are read together with the position:
+  // none of these loads waits for another.
   const std::uint32_t pc = p0 < kv.capacity ? p0 : kv.capacity - 1u;
-  const std::uint32_t pl_pos = wp0 + pl < kv.capacity ? wp0 + pl : kv.capacity - 1u;
+  const std::uint32_t pr = wp0 + r < kv.capacity ? wp0 + r : kv.capacity - 1u;
   const std::uint32_t page_c = static_cast<std::uint32_t>(table[pc / kv.page_size]);
-  const std::uint32_t page_w = static_cast<std::uint32_t>(table[pl_pos / kv.page_size]);
+  const std::uint32_t page_r = static_cast<std::uint32_t>(table[pr / kv.page_size]);
   const std::uint32_t pos = pos_ptr[seq] < kv.capacity ? pos_ptr[seq] : kv.capacity - 1u;
   float* rec = partials + (static_cast<std::size_t>(g) * nchunks + c) * GROUP * (kHeadDim + 2u);
   if (p0 > pos) {  // chunk beyond the context (uniform over the workgroup): empty record
@@ -296,59 +301,59 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
       rec[i] = (i % (kHeadDim + 2u)) == 0u ? -INFINITY : 0.0f;
     return;
   }
-  const std::uint32_t npos = wp0 > pos ? 0u : ((pos - wp0 + 1u) < kAttnSub ? (pos - wp0 + 1u) : kAttnSub);
-  const bool valid = pl < npos;
   // K / V row offset (elements; the host checks that a layer's cache has fewer
-  // than 2^32 of them). A lane past the context reads the chunk's first row
-  // (inside the context, so finite data) and is weighted 0.
+  // than 2^32 of them). A position past the context reads the chunk's first
+  // row (inside the context, so finite data) and is weighted 0.
   auto row_of = [&](std::uint32_t page, std::uint32_t p) {
     return static_cast<std::uint32_t>(((static_cast<std::size_t>(page) * kv.n_kv + g) * kv.page_size +
                                        p % kv.page_size) * kHeadDim);
   };
-  const std::uint32_t row_off = valid ? row_of(page_w, pl_pos) : row_of(page_c, pc);
-  uint4 pk[4];
+  const std::uint32_t row_off = wp0 + r <= pos ? row_of(page_r, pr) : row_of(page_c, pc);
+  uint4 ka[4];  // A operands: K[position r][32 qq + 8 j + i]
   {
-    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off + (kHeadDim / 4u) * qd);
+    const uint4* kr = reinterpret_cast<const uint4*>(kv.k + row_off + 32u * qq);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) pk[w] = kr[w];
+    for (int j = 0; j < 4; ++j) ka[j] = kr[j];
   }
   std::uint32_t vw[kAttnSub];
 #pragma unroll
   for (int j = 0; j < static_cast<int>(kAttnSub); ++j) {
-    const std::uint32_t off = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_off), 4 * j));
+    const std::uint32_t off = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(row_off), j));
     vw[j] = *reinterpret_cast<const std::uint32_t*>(kv.v + off + 2u * lane);
   }
-  const float* qg = q + static_cast<std::size_t>(g) * GROUP * kHeadDim;
-  for (std::uint32_t i = threadIdx.x; i < GROUP * kHeadDim; i += blockDim.x) {
-    const std::uint32_t h = i / kHeadDim, d = i % kHeadDim;
-    qs[h][d / (kHeadDim / 4u)][d % (kHeadDim / 4u)] = qg[i];
+  // B operands, staged by the qkv epilogue (q16): column n = lane % 16 is
+  // head n / 2 (hi n even, lo n odd), rows = dims 32 qq + 8 j + i (A's order)
+  uint4 qb[4];
+  {
+    const uint4* qr = reinterpret_cast<const uint4*>(q + static_cast<std::size_t>(g) * kQ16PerKv) + lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qb[j] = qr[64 * j];
   }
-  __syncthreads();
-  const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
-  float s[GROUP];
+  f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h) s[h] = 0.0f;
+  for (int j = 0; j < 4; ++j)
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[j]), __builtin_bit_cast(half8, qb[j]), sc,
+                                                0, 0, 0);
+  // lane: column n, positions 4 qq + i; head hq's score = the hi + lo columns
+  float s4[4], p4[4];
+  float m = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const std::uint32_t words[4] = {pk[w].x, pk[w].y, pk[w].z, pk[w].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float k0 = h2f(words[e]), k1 = h2f(words[e] >> 16);
-      const int d = 8 * w + 2 * e;
-#pragma unroll
-      for (int h = 0; h < GROUP; ++h) s[h] += qs[h][qd][d] * k0 + qs[h][qd][d + 1] * k1;
-    }
+  for (int i = 0; i < 4; ++i) {
+    const float t = sc[i] + __shfl_xor(sc[i], 1, 64);
+    const bool valid = wp0 + 4u * qq + static_cast<std::uint32_t>(i) <= pos;
+    s4[i] = valid ? t : -INFINITY;
+    m = fmaxf(m, s4[i]);
   }
-  float pw[GROUP], mh[GROUP], lh[GROUP];
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, __shfl_xor(m, 32, 64));  // head max over the wave's positions (-inf: none)
+  float l = 0.0f;
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h) {
-    float sh = s[h] + __shfl_xor(s[h], 1, 64);
-    sh += __shfl_xor(sh, 2, 64);
-    const float sc = valid ? sh * scale : -INFINITY;
-    mh[h] = wave_max(sc);  // -inf for a wave without positions
-    pw[h] = valid ? expf(sc - mh[h]) : 0.0f;
-    lh[h] = wave_sum(qd == 0u ? pw[h] : 0.0f);
+  for (int i = 0; i < 4; ++i) {
+    p4[i] = s4[i] == -INFINITY ? 0.0f : expf(s4[i] - m);
+    l += p4[i];
   }
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
   float o0[GROUP], o1[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
@@ -357,23 +362,25 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
     const float v0 = h2f(vw[j]), v1 = h2f(vw[j] >> 16);
 #pragma unroll
     for (int h = 0; h < GROUP; ++h) {
-      const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw[h]), 4 * j));
+      // p of position j, head h: lane 16 (j / 4) + 2 h, register j % 4
+      const float p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p4[j & 3]),
+                                                                          16 * (j >> 2) + 2 * h));
       o0[h] += p * v0;
       o1[h] += p * v1;
     }
   }
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h) {
+  for (int h = 0; h < GROUP; ++h)
     *reinterpret_cast<float2*>(&wrec[wave][h][2u + 2u * lane]) = make_float2(o0[h], o1[h]);
-    if (lane == 0u) {
-      wrec[wave][h][0] = mh[h];
-      wrec[wave][h][1] = lh[h];
-    }
+  if (lane < 2u * GROUP && (lane & 1u) == 0u) {
+    wrec[wave][lane >> 1][0] = m;
+    wrec[wave][lane >> 1][1] = l;
   }
   __syncthreads();
-  if (wave != 0u) return;
-#pragma unroll
-  for (int h = 0; h < GROUP; ++h) {
+  // wave h merges head h's records
+  if (wave >= static_cast<std::uint32_t>(GROUP)) return;
+  {
+    const std::uint32_t h = wave;
     float M = wrec[0][h][0];  // finite: wave 0 holds position p0
 #pragma unroll
     for (std::uint32_t w = 1; w < kAttnWaves; ++w) M = fmaxf(M, wrec[w][h][0]);
@@ -386,11 +393,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const flo
       a0 += f * o.x;
       a1 += f * o.y;
     }
-    float* r = rec + h * (kHeadDim + 2u);
-    *reinterpret_cast<float2*>(r + 2u + 2u * lane) = make_float2(a0, a1);
+    float* rr = rec + h * (kHeadDim + 2u);
+    *reinterpret_cast<float2*>(rr + 2u + 2u * lane) = make_float2(a0, a1);
     if (lane == 0u) {
-      r[0] = M;
-      r[1] = L;
+      rr[0] = M;
+      rr[1] = L;
     }
   }
 }
@@ -549,14 +556,16 @@ hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::
 
 hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
                       const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
-                      std::uint32_t rope_positions, const std::uint32_t* pos, float* q_out, const KvLayer& kv,
+                      std::uint32_t rope_positions, const std::uint32_t* pos, void* q_out, const KvLayer& kv,
                       hipStream_t stream) {
-  if (rope == nullptr || rope_positions == 0u) return hipErrorInvalidValue;
+  if (rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || q_rows % (kHeadDim * kv.n_kv) != 0u)
+    return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
   EpiQkv e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps;
   e.q_rows = q_rows, e.kv_rows = kv_rows, e.rope = rope, e.rope_positions = rope_positions;
-  e.pos_ptr = pos, e.q = q_out, e.kv = kv;
+  e.group = q_rows / kHeadDim / kv.n_kv;
+  e.pos_ptr = pos, e.q = static_cast<_Float16*>(q_out), e.kv = kv;
   return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, w.rows, e, stream);
 }
 
@@ -565,7 +574,7 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
   return static_cast<std::size_t>(n_kv) * nchunks * (n_heads / n_kv) * (kHeadDim + 2u);
 }
 
-hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                                   std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
                                   float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
@@ -578,11 +587,12 @@ hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32
   const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
   const std::size_t part = attention_partials_floats(n_heads, kv.n_kv, max_ctx);
   if (part > 0xFFFFFFFFull) return hipErrorInvalidValue;
-  const std::uint32_t part_stride = static_cast<std::uint32_t>(part), q_stride = n_heads * kHeadDim;
+  const std::uint32_t part_stride = static_cast<std::uint32_t>(part), q_stride = kv.n_kv * kQ16PerKv;
   const dim3 grid(nchunks, kv.n_kv, batch), block(64 * kAttnWaves);
 #define RTXLLM_ATTN_CASE(G)                                                                                      \
   case G:                                                                                                        \
-    hipLaunchKernelGGL(attn_partial_kernel<G>, grid, block, 0, stream, q, kv, pos, nchunks, partials, q_stride, \
+    hipLaunchKernelGGL(attn_partial_kernel<G>, grid, block, 0, stream, static_cast<const _Float16*>(q), kv, pos,   \
+                       nchunks, partials, q_stride,                                                              \
                        table_stride, part_stride);                                                               \
     break;
   switch (group) {
@@ -601,7 +611,7 @@ hipError_t launch_attention_batch(const float* q, const KvLayer& kv, std::uint32
   return hipGetLastError();
 }
 
-hipError_t launch_attention(const float* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
+hipError_t launch_attention(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                             std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (xq_att == nullptr) return hipErrorInvalidValue;
   return launch_attention_batch(q, kv, n_heads, pos, max_ctx, 1u, 0u, partials, att, xq_att, stream);

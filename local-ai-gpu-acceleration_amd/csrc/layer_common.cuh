@@ -38,6 +38,30 @@ __device__ __forceinline__ float2 rope_at(const float2* rope, std::uint32_t posi
   return rope[static_cast<std::size_t>(p) * (kHeadDim / 2u) + i];
 }
 
+// The rotated query as the attention's matrix-core operand ("q16"): per kv
+// head g, 4 instructions j x 64 lanes x 8 fp16, lane l = 16 (d / 32) + n
+// holding dims 32 (l / 16) + 8 j + i of column n = 2 h + part (h < group the
+// query head within g; part 0 = hi = fp16(x), 1 = lo = fp16(x - hi), x = q /
+// sqrt(head_dim)); columns n >= 2 group stay zero. kQ16PerKv values per kv head.
+constexpr std::uint32_t kQ16PerKv = 4u * 64u * 8u;
+static_assert(2u * kQ16PerKv == kQ16BytesPerKv, "q16 size");
+
+__device__ __forceinline__ std::size_t q16_index(std::uint32_t g, std::uint32_t h, std::uint32_t d,
+                                                 std::uint32_t part) {
+  const std::uint32_t l = 16u * (d >> 5) + 2u * h + part;
+  return ((static_cast<std::size_t>(g) * 4u + ((d >> 3) & 3u)) * 64u + l) * 8u + (d & 7u);
+}
+
+// Stores query value q (head `head` of n_heads = group * n_kv, dim d) into q16.
+__device__ __forceinline__ void q16_store(_Float16* q16, std::uint32_t head, std::uint32_t group, std::uint32_t d,
+                                          float q) {
+  const float x = q * 0.08838834764831845f;  // 1 / sqrt(128)
+  const _Float16 hi = static_cast<_Float16>(x);
+  const std::size_t i = q16_index(head / group, head % group, d, 0u);
+  q16[i] = hi;
+  q16[i + 8u] = static_cast<_Float16>(x - static_cast<float>(hi));  // column n + 1 = lane + 1
+}
+
 __device__ __forceinline__ std::uint16_t f2h(float v) {
   return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
 }

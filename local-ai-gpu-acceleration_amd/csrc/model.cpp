@@ -156,7 +156,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   specs.push_back({"h", 4u * B * c.hidden});
   specs.push_back({"xq", rtxllm::xq_bytes(c.hidden)});
   specs.push_back({"sumsq", 4u * m->nslots});
-  specs.push_back({"q", 4u * B * m->q_rows});
+  specs.push_back({"q", B * c.n_kv_heads * rtxllm::kQ16BytesPerKv});
   specs.push_back({"att", 4u * B * m->q_rows});
   specs.push_back({"xq_att", rtxllm::xq_bytes(m->q_rows)});
   specs.push_back({"attn_partials", 4u * B * m->partial_floats});
@@ -213,13 +213,17 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
                    hipMemcpyHostToDevice);
     if (st != hipSuccess) return st;
   }
-  if (batch > 1u) {  // staged columns of sequences >= batch stay zero
+  // staged columns of sequences >= batch and the q16 columns of absent query
+  // heads stay zero
+  for (const char* name : {"x16", "q"}) {
     std::size_t n = 0;
-    void* x16 = rtxllm_llama_region(m.get(), "x16", 0u, &n);
-    st = hipMemset(x16, 0, n);
-    if (st == hipSuccess) st = hipDeviceSynchronize();
+    void* p = rtxllm_llama_region(m.get(), name, 0u, &n);
+    if (p == nullptr) continue;
+    st = hipMemset(p, 0, n);
     if (st != hipSuccess) return st;
   }
+  st = hipDeviceSynchronize();
+  if (st != hipSuccess) return st;
   *out = m.release();
   return hipSuccess;
 }
@@ -299,11 +303,11 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
     case kQkv: {
       const TensorRef t = tensor(m, layer_name("qkv", l));
       return rtxllm::launch_mm_qkv_batch(c.fmt_qkv, t.payload, t.meta, c.hidden, x16, B, m->q_rows, m->kv_rows,
-                                         region<float2>(m, "rope"), c.max_ctx, pos, region<float>(m, "q"), kv_layer(m, l),
+                                         region<float2>(m, "rope"), c.max_ctx, pos, m->arena.arena_ptr("q"), kv_layer(m, l),
                                          m->pages_per_seq, stream);
     }
     case kAttention: {
-      hipError_t st = rtxllm::launch_attention_batch(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos,
+      hipError_t st = rtxllm::launch_attention_batch(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos,
                                                      c.max_ctx, B, m->pages_per_seq,
                                                      region<float>(m, "attn_partials"), region<float>(m, "att"),
                                                      nullptr, stream);
@@ -364,11 +368,11 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
     case kQkv: {
       const TensorRef t = tensor(m, layer_name("qkv", l));
       return rtxllm::launch_qkv(c.fmt_qkv, t.payload, t.meta, c.hidden, in, m->q_rows, m->kv_rows,
-                                region<float2>(m, "rope"), c.max_ctx, pos, region<float>(m, "q"), kv_layer(m, l),
+                                region<float2>(m, "rope"), c.max_ctx, pos, m->arena.arena_ptr("q"), kv_layer(m, l),
                                 stream);
     }
     case kAttention:
-      return rtxllm::launch_attention(region<float>(m, "q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
+      return rtxllm::launch_attention(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
                                       region<float>(m, "attn_partials"), region<float>(m, "att"),
                                       m->arena.arena_ptr("xq_att"), stream);
     case kO: {
