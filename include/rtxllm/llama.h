@@ -49,7 +49,9 @@ typedef struct {
 typedef struct rtxllm_llama rtxllm_llama;
 
 /* Allocate the arena on the current device (one hipMalloc) and set up the
- * RoPE table, identity KV block tables, token = 0, pos = 0. */
+ * RoPE table, identity KV block tables, token = 0, pos = 0. Strict admission
+ * first (include/rtxllm/admission.h): hipErrorOutOfMemory when weights + KV
+ * + workspace + graph memory exceed the device's free bytes. */
 hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out);
 void rtxllm_llama_destroy(rtxllm_llama* m);
 
@@ -87,6 +89,25 @@ hipError_t rtxllm_llama_download(rtxllm_llama* m, const char* name, uint32_t lay
  * seed + 6; d, dmin = fp16(U[1e-4, 2e-3]). Norm weights and the KV cache are
  * left to the caller. Q4_K split layouts other than split-native are refused. */
 hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_t stream);
+
+/* Fill every weight tensor from resident packs: the Q4_K manifest and the
+ * raw-block (IQ2_S / IQ3_S / Q5_K) manifest of the pack producers
+ * (tools/bench/q4k_resident_pack.py, iq_resident_pack.py schema; either may be
+ * null), pack paths relative to payload_root unless absolute. Tensors by GGUF
+ * name: blk.<l>.attn_q / attn_k / attn_v (stacked into "qkv"), attn_output,
+ * ffn_gate / ffn_up (interleaved into "gate_up"), ffn_down, token_embd and
+ * output (".weight"). Each must be in the configured format (a Q4_K split
+ * layout's pack policy must match it; raw Q4_K comes from blocks_path) with
+ * the model's shape, and every file's size and byte-sum checksum must match
+ * its manifest. hipErrorInvalidValue with the reason in err otherwise. */
+hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_manifest, const char* iq_manifest,
+                                   const char* payload_root, char* err, size_t err_len);
+
+/* The admission check made at create: bytes the model needs (weights, KV,
+ * workspace, graph), the device bytes it was admitted against, and the arena
+ * size. */
+hipError_t rtxllm_llama_memory(const rtxllm_llama* m, size_t* required_bytes, size_t* usable_bytes,
+                               size_t* arena_bytes);
 
 enum { RTXLLM_LLAMA_EMBED = 1, RTXLLM_LLAMA_HEAD = 2 };
 

@@ -9,15 +9,20 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <new>
 #include <string>
 #include <vector>
 
 #include "layer.h"
+#include "rtxllm/admission.h"
 #include "rtxllm/decode_kernels.h"
 #include "rtxllm/hip_graph_bucket.h"
+#include "rtxllm/layer_executor.h"
+#include "rtxllm/layer_plan.h"
 #include "rtxllm/llama.h"
+#include "rtxllm/pack_manifest.h"
 #include "rtxllm/vram_arena.h"
 #include "synth.h"
 #include "xq.h"
@@ -31,6 +36,11 @@ struct rtxllm_llama {
   std::size_t partial_floats = 0;  // attention partial records per sequence
   std::uint32_t batch = 1, pages_per_seq = 0;
   std::uint32_t groups_o = 1, groups_down = 1;  // panel groups of the batch o / down matvecs
+  // role plans of the layer-slice executor: one decoder layer (attention
+  // phase: qkv (+ attention), o; ffn phase: gate/up, down) and the head
+  // (output phase: LM head + argmax)
+  rtxllm::LayerExecutionPlan layer_plan, head_plan;
+  rtxllm::AdmissionDecision admission;
 };
 
 namespace {
@@ -178,6 +188,46 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   }
   specs.push_back({"inv_freq", 4u * rtxllm::kHeadDim / 2u});
   specs.push_back({"rope", 8u * static_cast<std::size_t>(c.max_ctx) * (rtxllm::kHeadDim / 2u)});
+  // the layer-slice role plans, validated once
+  {
+    static const std::vector<rtxllm::LayerStageDescriptor> kLayer = {
+        {"attn_qkv.weight"}, {"attn_output.weight"}, {"ffn_gate_up.weight"}, {"ffn_down.weight"}};
+    static const std::vector<rtxllm::LayerStageDescriptor> kHeadStages = {{"output.weight", false}};
+    for (const auto* stages : {&kLayer, &kHeadStages}) {
+      const auto segments = rtxllm::build_layer_phase_segments(*stages);
+      if (stages == &kLayer && !rtxllm::validate_layer_phase_plan(*stages, segments).passed)
+        return hipErrorInvalidValue;
+      (stages == &kLayer ? m->layer_plan : m->head_plan) = rtxllm::build_layer_execution_plan(segments, false);
+    }
+  }
+  // strict admission: weights, KV cache, workspace and the step graph's
+  // memory against the device's free bytes
+  {
+    rtxllm::RequestEstimate req;
+    for (const auto& spec : specs) {
+      const std::size_t b = (spec.bytes + 255u) & ~std::size_t{255};
+      const std::string& n = spec.name;
+      const bool kv = n.find("k_cache") != std::string::npos || n.find("v_cache") != std::string::npos ||
+                      n.find("block_table") != std::string::npos;
+      const bool weight = n.find(".qkv") != std::string::npos || n.find(".o") != std::string::npos ||
+                          n.find(".gate_up") != std::string::npos || n.find(".down") != std::string::npos ||
+                          n.find("_norm") != std::string::npos || n == "embed" || n.rfind("lm_head", 0) == 0;
+      (kv ? req.kv_cache_bytes : weight ? req.weight_bytes : req.workspace_bytes) += b;
+    }
+    req.workspace_high_water_bytes = req.workspace_bytes;
+    rtxllm::HipGraphBucketDescriptor gd;
+    gd.name = "decode";
+    gd.batch_bucket = batch;
+    gd.phase_count = static_cast<std::uint32_t>(c.n_layers * m->layer_plan.phase_count + m->head_plan.phase_count);
+    gd.kernel_launches_per_replay = batch > 1u ? 1u + 10u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
+    gd.workspace_high_water_bytes = req.workspace_bytes;
+    req.graph_bytes = rtxllm::estimate_hip_graph_bucket_allocation(gd).total_bytes;
+    std::size_t free_b = 0, total_b = 0;
+    const hipError_t mi = hipMemGetInfo(&free_b, &total_b);
+    if (mi != hipSuccess) return mi;
+    m->admission = rtxllm::decide_admission(rtxllm::ResidencyPolicy::Strict, rtxllm::MemoryBudget{free_b, 0}, req);
+    if (!m->admission.admit) return hipErrorOutOfMemory;
+  }
   try {
     m->arena.initialize(specs);
     m->arena.reset();
@@ -261,6 +311,184 @@ extern "C" hipError_t rtxllm_llama_download(rtxllm_llama* m, const char* name, u
   auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
   if (base == nullptr || dst == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
   return hipMemcpy(dst, base + offset, bytes, hipMemcpyDeviceToHost);
+}
+
+namespace {
+
+// One tensor read from a pack: its format, GGUF shape and stream bytes.
+struct PackTensor {
+  int fmt = -1;
+  std::uint64_t rows = 0, cols = 0;
+  std::vector<std::uint8_t> payload, meta;
+};
+
+std::filesystem::path under(const std::filesystem::path& root, const std::filesystem::path& p) {
+  return p.is_absolute() || root.empty() ? p : root / p;
+}
+
+void verify(const std::vector<std::uint8_t>& bytes, std::uint64_t checksum, const std::string& what) {
+  if (rtxllm::byte_checksum(bytes) != checksum) throw std::runtime_error("checksum mismatch: " + what);
+}
+
+// GGUF tensors of the manifests, by name. A Q4_K tensor is read in the layout
+// the runner's config wants for it (`want` maps a tensor name to its format):
+// a split layout from its payload + metadata files (the manifest's policy
+// must be that layout), the raw blocks from blocks_path.
+std::map<std::string, PackTensor> read_packs(const char* q4k_manifest, const char* iq_manifest,
+                                             const std::filesystem::path& root,
+                                             const std::map<std::string, int>& want) {
+  std::map<std::string, PackTensor> out;
+  if (q4k_manifest != nullptr && *q4k_manifest != '\0') {
+    const rtxllm::Q4KManifest man = rtxllm::load_q4k_manifest(q4k_manifest);
+    for (const auto& t : man.tensors) {
+      const auto w = want.find(t.name);
+      if (w == want.end()) continue;
+      PackTensor pt;
+      pt.fmt = w->second;
+      pt.rows = t.rows, pt.cols = t.cols;
+      const std::uint64_t blocks = static_cast<std::uint64_t>(t.rows) * (t.cols / 256u);
+      if (pt.fmt == RTXLLM_FMT_Q4K_RAW) {
+        if (t.blocks_path.empty()) throw std::runtime_error("raw Q4_K blocks not in the pack: " + t.name);
+        pt.payload = rtxllm::load_binary_file(under(root, t.blocks_path), blocks * 144u, "q4k blocks");
+        verify(pt.payload, t.source_checksum, t.name + " blocks");
+      } else {
+        if (rtxllm::q4k_policy_format(t.policy) != pt.fmt)
+          throw std::runtime_error("Q4_K pack layout " + t.policy + " is not the configured one: " + t.name);
+        pt.payload = rtxllm::load_binary_file(under(root, t.payload_path), t.payload_bytes, "q4k payload");
+        pt.meta = rtxllm::load_binary_file(under(root, t.metadata_path), t.metadata_bytes, "q4k metadata");
+        verify(pt.payload, t.payload_checksum, t.name + " payload");
+        verify(pt.meta, t.metadata_checksum, t.name + " metadata");
+        if (pt.payload.size() != blocks * rtxllm_format_payload_bytes(pt.fmt) ||
+            pt.meta.size() != blocks * rtxllm_format_meta_bytes(pt.fmt))
+          throw std::runtime_error("Q4_K pack stream sizes disagree with the shape: " + t.name);
+      }
+      out[t.name] = std::move(pt);
+    }
+  }
+  if (iq_manifest != nullptr && *iq_manifest != '\0') {
+    const rtxllm::IQManifest man = rtxllm::load_iq_manifest(iq_manifest);
+    static const std::map<std::string, int> kType = {
+        {"IQ2_S", RTXLLM_FMT_IQ2S}, {"IQ3_S", RTXLLM_FMT_IQ3S}, {"Q5_K", RTXLLM_FMT_Q5K}};
+    for (const auto& t : man.tensors) {
+      const auto w = want.find(t.name);
+      if (w == want.end()) continue;
+      PackTensor pt;
+      pt.fmt = kType.at(t.type);
+      if (pt.fmt != w->second) throw std::runtime_error("pack type " + t.type + " is not the configured one: " + t.name);
+      if (t.dimensions.size() != 2u) throw std::runtime_error("raw-block pack without 2-D dimensions: " + t.name);
+      pt.cols = t.dimensions[0], pt.rows = t.dimensions[1];
+      if (t.block_count != pt.rows * (pt.cols / 256u) || t.block_type_size != rtxllm_format_payload_bytes(pt.fmt))
+        throw std::runtime_error("raw-block pack geometry disagrees with its dimensions: " + t.name);
+      pt.payload = rtxllm::load_binary_file(under(root, t.payload_path), t.payload_bytes, "raw blocks");
+      verify(pt.payload, t.payload_checksum, t.name);
+      out[t.name] = std::move(pt);
+    }
+  }
+  return out;
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_manifest, const char* iq_manifest,
+                                              const char* payload_root, char* err, size_t err_len) {
+  auto report = [&](const std::string& what) {
+    if (err != nullptr && err_len > 0) {
+      const std::size_t n = std::min(what.size(), err_len - 1u);
+      std::memcpy(err, what.data(), n);
+      err[n] = '\0';
+    }
+  };
+  if (m == nullptr) return hipErrorInvalidValue;
+  const rtxllm_llama_config& c = m->cfg;
+  const std::uint32_t H = c.hidden, Q = m->q_rows, KV = m->kv_rows, F = c.ffn;
+  // every tensor the model needs: GGUF name -> (format, rows, cols)
+  struct Need {
+    int fmt;
+    std::uint64_t rows, cols;
+  };
+  std::map<std::string, Need> need;
+  for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+    const std::string b = "blk." + std::to_string(l) + ".";
+    need[b + "attn_q.weight"] = {c.fmt_qkv, Q, H};
+    need[b + "attn_k.weight"] = {c.fmt_qkv, KV, H};
+    need[b + "attn_v.weight"] = {c.fmt_qkv, KV, H};
+    need[b + "attn_output.weight"] = {c.fmt_o, H, Q};
+    need[b + "ffn_gate.weight"] = {c.fmt_gate_up, F, H};
+    need[b + "ffn_up.weight"] = {c.fmt_gate_up, F, H};
+    need[b + "ffn_down.weight"] = {c.fmt_down, H, F};
+  }
+  need["token_embd.weight"] = {RTXLLM_FMT_Q5K, c.vocab, H};
+  need["output.weight"] = {c.fmt_lm_head, c.vocab, H};
+  std::map<std::string, int> want;
+  for (const auto& kv : need) want[kv.first] = kv.second.fmt;
+  try {
+    const auto packs = read_packs(q4k_manifest, iq_manifest, payload_root != nullptr ? payload_root : "", want);
+    auto get = [&](const std::string& name) -> const PackTensor& {
+      const auto it = packs.find(name);
+      if (it == packs.end()) throw std::runtime_error("tensor missing from the packs: " + name);
+      const Need& n = need.at(name);
+      if (it->second.rows != n.rows || it->second.cols != n.cols)
+        throw std::runtime_error("tensor shape disagrees with the model: " + name);
+      return it->second;
+    };
+    auto put = [&](const std::string& region, const std::vector<std::uint8_t>& bytes) {
+      if (bytes.empty()) return;
+      std::size_t size = 0;
+      void* dst = rtxllm_llama_region(m, region.c_str(), 0u, &size);
+      if (dst == nullptr || size != bytes.size()) throw std::runtime_error("region size mismatch: " + region);
+      const hipError_t st = hipMemcpy(dst, bytes.data(), bytes.size(), hipMemcpyHostToDevice);
+      if (st != hipSuccess) throw std::runtime_error(std::string("upload failed: ") + hipGetErrorString(st));
+    };
+    // stack rows (q | k | v) or interleave them (gate_i, up_i) stream by stream
+    auto stack = [](std::initializer_list<const std::vector<std::uint8_t>*> parts) {
+      std::vector<std::uint8_t> out;
+      for (const auto* p : parts) out.insert(out.end(), p->begin(), p->end());
+      return out;
+    };
+    auto interleave = [](const std::vector<std::uint8_t>& a, const std::vector<std::uint8_t>& b, std::size_t rows) {
+      std::vector<std::uint8_t> out(a.size() + b.size());
+      if (rows == 0 || a.size() != b.size() || a.size() % rows != 0) throw std::runtime_error("gate/up streams differ");
+      const std::size_t rb = a.size() / rows;
+      for (std::size_t i = 0; i < rows; ++i) {
+        std::memcpy(out.data() + (2 * i) * rb, a.data() + i * rb, rb);
+        std::memcpy(out.data() + (2 * i + 1) * rb, b.data() + i * rb, rb);
+      }
+      return out;
+    };
+    for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+      const std::string b = "blk." + std::to_string(l) + ".", L = "L" + std::to_string(l) + ".";
+      const auto &q = get(b + "attn_q.weight"), &k = get(b + "attn_k.weight"), &v = get(b + "attn_v.weight");
+      put(L + "qkv", stack({&q.payload, &k.payload, &v.payload}));
+      put(L + "qkv_meta", stack({&q.meta, &k.meta, &v.meta}));
+      const auto& o = get(b + "attn_output.weight");
+      put(L + "o", o.payload);
+      put(L + "o_meta", o.meta);
+      const auto &g = get(b + "ffn_gate.weight"), &u = get(b + "ffn_up.weight");
+      put(L + "gate_up", interleave(g.payload, u.payload, F));
+      if (!g.meta.empty()) put(L + "gate_up_meta", interleave(g.meta, u.meta, F));
+      const auto& d = get(b + "ffn_down.weight");
+      put(L + "down", d.payload);
+      put(L + "down_meta", d.meta);
+    }
+    put("embed", get("token_embd.weight").payload);
+    const auto& lm = get("output.weight");
+    put("lm_head", lm.payload);
+    put("lm_head_meta", lm.meta);
+  } catch (const std::exception& e) {
+    report(e.what());
+    return hipErrorInvalidValue;
+  }
+  report("");
+  return hipSuccess;
+}
+
+extern "C" hipError_t rtxllm_llama_memory(const rtxllm_llama* m, size_t* required_bytes, size_t* usable_bytes,
+                                          size_t* arena_bytes) {
+  if (m == nullptr) return hipErrorInvalidValue;
+  if (required_bytes != nullptr) *required_bytes = m->admission.required_bytes;
+  if (usable_bytes != nullptr) *usable_bytes = m->admission.usable_bytes;
+  if (arena_bytes != nullptr) *arena_bytes = m->arena.total_bytes();
+  return hipSuccess;
 }
 
 extern "C" hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_t stream) {
@@ -412,12 +640,34 @@ extern "C" hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint
   const float* out_norm = region<float>(m, "out_norm");
   const float* first_norm = first < last ? region<float>(m, layer_name("attn_norm", first)) : out_norm;
   hipError_t st = launch_stage(m, 0u, kEmbed, (flags & RTXLLM_LLAMA_EMBED) != 0, first_norm, stream);
-  for (std::uint32_t l = first; l < last && st == hipSuccess; ++l) {
-    const float* next_norm = l + 1u < last ? region<float>(m, layer_name("attn_norm", l + 1u)) : out_norm;
-    for (int stage = kQkv; stage <= kDown && st == hipSuccess; ++stage)
-      st = launch_stage(m, l, stage, false, next_norm, stream);
+  // Each layer replays the layer plan by phase: stage i of the plan is one of
+  // qkv (with the attention over the updated cache), o, gate/up, down (their
+  // activation hand-off is fused into the stages, so no feedback launches).
+  static constexpr int kLayerStages[] = {kQkv, kO, kGateUp, kDown};
+  try {
+    for (std::uint32_t l = first; l < last && st == hipSuccess; ++l) {
+      const float* next_norm = l + 1u < last ? region<float>(m, layer_name("attn_norm", l + 1u)) : out_norm;
+      auto launch = [&](std::size_t i) {
+        if (st == hipSuccess) st = launch_stage(m, l, kLayerStages[i], false, next_norm, stream);
+        if (st == hipSuccess && kLayerStages[i] == kQkv) st = launch_stage(m, l, kAttention, false, next_norm, stream);
+      };
+      auto phase = [&](const rtxllm::LayerPhaseExecution& p) {
+        return rtxllm::replay_layer_phase(p, m->layer_plan.stage_count, launch, [](std::size_t) {});
+      };
+      auto none = [](const rtxllm::LayerPhaseExecution&) -> rtxllm::LayerReplayCounters {
+        throw std::runtime_error("the decoder layer has no such phase");
+      };
+      rtxllm::replay_layer_execution_plan_by_phase(m->layer_plan, m->layer_plan.stage_count, phase, phase, none, none);
+    }
+    if (st == hipSuccess && (flags & RTXLLM_LLAMA_HEAD)) {
+      auto head = [&](std::size_t) {
+        if (st == hipSuccess) st = launch_stage(m, 0u, kHead, false, out_norm, stream);
+      };
+      rtxllm::replay_layer_execution_plan(m->head_plan, m->head_plan.stage_count, head, [](std::size_t) {});
+    }
+  } catch (const std::exception&) {
+    return hipErrorInvalidValue;
   }
-  if (st == hipSuccess && (flags & RTXLLM_LLAMA_HEAD)) st = launch_stage(m, 0u, kHead, false, out_norm, stream);
   return st;
 }
 

@@ -47,6 +47,8 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_graph_capture": [_P, _S],
     "rtxllm_llama_graph_replay": [_P, _S],
     "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
+    "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
+    "rtxllm_llama_memory": [_P, _P, _P, _P],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",

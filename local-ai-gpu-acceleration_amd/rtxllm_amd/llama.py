@@ -140,6 +140,23 @@ class Llama:
     def launch_stage(self, layer: int, stage: str, stream: int = 0) -> None:
         check("rtxllm_llama_launch_stage", lib().rtxllm_llama_launch_stage(self.h, layer, self.STAGES[stage], stream))
 
+    def load_packs(self, q4k_manifest=None, iq_manifest=None, payload_root=None) -> None:
+        """Fill the weights from resident-pack manifests (include/rtxllm/llama.h)."""
+        err = ctypes.create_string_buffer(1024)
+        enc = lambda p: None if p is None else str(p).encode()
+        rc = lib().rtxllm_llama_load_packs(self.h, enc(q4k_manifest), enc(iq_manifest), enc(payload_root), err,
+                                           len(err))
+        if rc != 0:
+            from ._lib import HipError
+            raise HipError(f"rtxllm_llama_load_packs: {err.value.decode(errors='replace')}", rc)
+
+    def memory(self) -> dict:
+        """The create-time admission figures: required, usable and arena bytes."""
+        req, use, arena = c_size_t(), c_size_t(), c_size_t()
+        check("rtxllm_llama_memory", lib().rtxllm_llama_memory(self.h, ctypes.byref(req), ctypes.byref(use),
+                                                               ctypes.byref(arena)))
+        return {"required_bytes": req.value, "usable_bytes": use.value, "arena_bytes": arena.value}
+
     def launches_per_step(self) -> int:
         return int(lib().rtxllm_llama_launches_per_step(self.h))
 
