@@ -65,10 +65,12 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
 // The same for `batch` sequences: sequence s has q16 n_kv * kQ16BytesPerKv
 // bytes on, block-table row s (table_stride entries, >= capacity /
 // page_size), position pos[s], and writes att[s]; xq_att must be null when
-// batch > 1 (the batch step stages att with launch_stage_batch).
+// batch > 1. x16_att (batch <= 8, xq_att null): att of every sequence is also
+// staged there for the batched o projection (the launch_stage_batch rule;
+// sequences >= batch zero), in the same launch as the combine.
 hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                                   std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
-                                  float* partials, float* att, void* xq_att, hipStream_t stream);
+                                  float* partials, float* att, void* xq_att, void* x16_att, hipStream_t stream);
 
 // h += W x (rows % 16 == 0), x either the staged input xq_in or the fp32 x_in
 // (staged by each wave itself; exactly one of the two non-null); then xq_next =

@@ -17,6 +17,7 @@
 #include "layer.h"
 #include "layer_common.cuh"
 #include "mv_launch.cuh"
+#include "x16.h"
 
 namespace rtxllm {
 namespace {
@@ -404,20 +405,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
 
 constexpr std::uint32_t kCombinePass = 32;  // chunk records per combine pass
 
-// One wave per query head: merge the chunk records (m_c, l_c, o_c) of its kv
-// head into att = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c. Per pass of 32
+// Merge the chunk records (m_c, l_c, o_c) of one query head (head of its kv
+// head's group) into the lane's two dimensions 2 lane, 2 lane + 1 of att =
+// sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c; one wave. Per pass of 32
 // chunks every load is issued up front: lane c reads chunk c's (m, l) (wave max
 // / sum) and, as lane = dimension pair, the pass's 32 o_c rows; the weights are
 // taken by readlane. Running sums are rescaled when a later pass raises the
-// maximum. Sequence blockIdx.y of a batch reads its records part_stride floats
-// on and writes att (n_heads * head_dim per sequence) further on; xq (batch 1
-// only) is skipped when null.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
-                                                          std::uint32_t nchunks, float* __restrict__ att, XQOut xq,
-                                                          std::uint32_t part_stride) {
-  const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
-  partials += static_cast<std::size_t>(blockIdx.y) * part_stride;
-  att += static_cast<std::size_t>(blockIdx.y) * gridDim.x * kHeadDim;
+// maximum.
+__device__ __forceinline__ float2 combine_head(const float* __restrict__ partials, std::uint32_t group,
+                                               std::uint32_t nchunks, std::uint32_t head, std::uint32_t lane) {
   const std::uint32_t g = head / group, hh = head % group;
   // every chunk record is merged: chunks past the context hold (-inf, 0, 0),
   // so the kernel needs no position and starts loading at once
@@ -451,7 +447,20 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
       o1 += wj * ov[j].y;
     }
   }
-  const float a0 = o0 / L, a1 = o1 / L;
+  return make_float2(o0 / L, o1 / L);
+}
+
+// One wave per query head (blockIdx.x): att of the head. Sequence blockIdx.y
+// of a batch reads its records part_stride floats on and writes att (n_heads *
+// head_dim per sequence) further on; xq (batch 1 only) is skipped when null.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ partials, std::uint32_t group,
+                                                          std::uint32_t nchunks, float* __restrict__ att, XQOut xq,
+                                                          std::uint32_t part_stride) {
+  const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
+  partials += static_cast<std::size_t>(blockIdx.y) * part_stride;
+  att += static_cast<std::size_t>(blockIdx.y) * gridDim.x * kHeadDim;
+  const float2 a = combine_head(partials, group, nchunks, head, lane);
+  const float a0 = a.x, a1 = a.y;
   const std::uint32_t d0 = head * kHeadDim + 2u * lane;
   *reinterpret_cast<float2*>(att + d0) = make_float2(a0, a1);
   if (xq.h == nullptr) return;  // the whole grid: a batch stages att separately
@@ -486,6 +495,53 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     xq.s[t] = s;
     xq.sum[t] = s * static_cast<float>(total);
   }
+}
+
+// Batch form with the o projection's staging fused: wave w of workgroup
+// (b, s) combines head 2 b + w of sequence s, so the workgroup holds the 256
+// columns of x16 block b (two heads): att, then the block's exponent from its
+// max |att| and the hi / lo fp16 pairs in operand order (the rule of the batch
+// staging kernel, no norm). Sequences s >= batch (grid y is 8) write zero
+// columns and exponent 0.
+__global__ __launch_bounds__(128) void attn_combine_x16_kernel(const float* __restrict__ partials, std::uint32_t group,
+                                                               std::uint32_t nchunks, std::uint32_t batch,
+                                                               float* __restrict__ att, _Float16* __restrict__ x16,
+                                                               std::uint32_t part_stride) {
+  __shared__ float pm[2];
+  const std::uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const std::uint32_t b = blockIdx.x, s = blockIdx.y, head = 2u * b + wave;
+  const std::uint32_t cols = 2u * gridDim.x * kHeadDim, c0 = head * kHeadDim + 2u * lane;
+  const X16Tail tail = x16_tail(x16, cols);
+  if (b == 0u && s == 0u && threadIdx.x == 0u) *tail.eps = -1.0f;
+  if (s >= batch) {
+#pragma unroll
+    for (std::uint32_t j = 0; j < 2u; ++j) {
+      const std::size_t i = x16_index(2u * s, c0 + j);
+      x16[i] = x16[i + 8u] = static_cast<_Float16>(0.0f);
+    }
+    if (threadIdx.x == 0u) {
+      tail.e[s * (cols / 256u) + b] = 0;
+      tail.ss[s * (cols / 256u) + b] = 0.0f;
+    }
+    return;
+  }
+  const float2 a = combine_head(partials + static_cast<std::size_t>(s) * part_stride, group, nchunks, head, lane);
+  *reinterpret_cast<float2*>(att + static_cast<std::size_t>(s) * cols + c0) = a;
+  float m = wave_max(fmaxf(fabsf(a.x), fabsf(a.y)));
+  if (lane == 0u) pm[wave] = m;
+  __syncthreads();
+  m = fmaxf(pm[0], pm[1]);
+  int e = 0;
+  if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+  const float v[2] = {ldexpf(a.x, -e), ldexpf(a.y, -e)};
+#pragma unroll
+  for (std::uint32_t j = 0; j < 2u; ++j) {
+    const _Float16 hi = static_cast<_Float16>(v[j]);
+    const std::size_t i = x16_index(2u * s, c0 + j);
+    x16[i] = hi;
+    x16[i + 8u] = static_cast<_Float16>(v[j] - static_cast<float>(hi));  // column 2 s + 1
+  }
+  if (threadIdx.x == 0u) tail.e[s * (cols / 256u) + b] = e;
 }
 
 // One workgroup of 256 per sequence (blockIdx.x, keys key_stride apart): the
@@ -576,10 +632,12 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
 
 hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                                   std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
-                                  float* partials, float* att, void* xq_att, hipStream_t stream) {
+                                  float* partials, float* att, void* xq_att, void* x16_att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
       kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u || batch == 0u ||
       batch > 65535u || (batch > 1u && (xq_att != nullptr || table_stride < kv.capacity / kv.page_size)))
+    return hipErrorInvalidValue;
+  if (x16_att != nullptr && (xq_att != nullptr || batch > kBatchMax || (n_heads * kHeadDim) % 256u != 0u))
     return hipErrorInvalidValue;
   // element offsets of a layer's K / V cache (every sequence's pages) fit 32 bits
   if (static_cast<std::uint64_t>(kv.capacity) * batch * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
@@ -605,6 +663,11 @@ hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_
 #undef RTXLLM_ATTN_CASE
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
+  if (x16_att != nullptr) {
+    hipLaunchKernelGGL(attn_combine_x16_kernel, dim3(n_heads / 2u, kBatchMax), dim3(128), 0, stream, partials, group,
+                       nchunks, batch, att, static_cast<_Float16*>(x16_att), part_stride);
+    return hipGetLastError();
+  }
   const XQOut xq = xq_att != nullptr ? xq_out(xq_att, n_heads * kHeadDim) : XQOut{};
   hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads, batch), dim3(64), 0, stream, partials, group, nchunks, att, xq,
                      part_stride);
@@ -614,7 +677,7 @@ hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_
 hipError_t launch_attention(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
                             std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (xq_att == nullptr) return hipErrorInvalidValue;
-  return launch_attention_batch(q, kv, n_heads, pos, max_ctx, 1u, 0u, partials, att, xq_att, stream);
+  return launch_attention_batch(q, kv, n_heads, pos, max_ctx, 1u, 0u, partials, att, xq_att, nullptr, stream);
 }
 
 hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,

@@ -219,7 +219,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     gd.name = "decode";
     gd.batch_bucket = batch;
     gd.phase_count = static_cast<std::uint32_t>(c.n_layers * m->layer_plan.phase_count + m->head_plan.phase_count);
-    gd.kernel_launches_per_replay = batch > 1u ? 1u + 10u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
+    gd.kernel_launches_per_replay = batch > 1u ? 1u + 9u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
     gd.workspace_high_water_bytes = req.workspace_bytes;
     req.graph_bytes = rtxllm::estimate_hip_graph_bucket_allocation(gd).total_bytes;
     std::size_t free_b = 0, total_b = 0;
@@ -535,12 +535,9 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
                                          m->pages_per_seq, stream);
     }
     case kAttention: {
-      hipError_t st = rtxllm::launch_attention_batch(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos,
-                                                     c.max_ctx, B, m->pages_per_seq,
-                                                     region<float>(m, "attn_partials"), region<float>(m, "att"),
-                                                     nullptr, stream);
-      if (st != hipSuccess) return st;
-      return rtxllm::launch_stage_batch(region<float>(m, "att"), B, m->q_rows, x16, stream);
+      return rtxllm::launch_attention_batch(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx, B,
+                                            m->pages_per_seq, region<float>(m, "attn_partials"),
+                                            region<float>(m, "att"), nullptr, x16, stream);
     }
     case kO: {
       const TensorRef t = tensor(m, layer_name("o", l));
@@ -687,7 +684,7 @@ extern "C" hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream) {
 extern "C" uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m) {
   if (m == nullptr) return 0u;
   // batch: qkv 1, attention 3 (partials, combine, staging), o / gate-up / down 2 each
-  return m->batch > 1u ? 1u + 10u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
+  return m->batch > 1u ? 1u + 9u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
 }
 
 extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream) {
