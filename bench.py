@@ -45,6 +45,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 256 MiB device copy and each decode stage of layer 0 a few times (for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), print nothing else")
+    ap.add_argument("--q4k-sweep", action="store_true",
+                    help="time every Q4_K resident layout at the config shapes (HBM-cold, rotating copies) and "
+                         "print the fastest per shape as JSON, nothing else")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -291,37 +294,70 @@ def traffic_of(stage: str):
 
 # ---- matvec set -----------------------------------------------------------------
 
-def matvec_set_bench(torch) -> dict:
-    from rtxllm_amd import formats as F
+def time_matvec(torch, stream, fmt: int, rows: int, cols: int, seed: int) -> tuple[float, int, int]:
+    """Mean us of one batch-1 matvec (staged x) over rotating weight copies
+    spanning more than twice the MALL, so every launch reads HBM; also the
+    copy count and the layout's resident bytes."""
     from rtxllm_amd import ops, packs
 
     dev = "cuda:0"
+    pack = packs.make_pack(fmt, rows, cols, seed)
+    base = ops.DevicePack(pack, dev)
+    nbytes = pack.payload.nbytes + (pack.meta.nbytes if pack.meta is not None else 0)
+    copies = [base]
+    while len(copies) * nbytes < 2 * MALL_BYTES + nbytes:
+        c = ops.DevicePack.__new__(ops.DevicePack)
+        c.fmt, c.rows, c.cols = base.fmt, base.rows, base.cols
+        c.payload = base.payload.clone()
+        c.meta = base.meta.clone() if base.meta is not None else None
+        copies.append(c)
+    xq = ops.stage(ops.to_dev(packs.normal_f32(seed + 0x100, cols), dev))
+    y = torch.empty(rows, dtype=torch.float32, device=dev)
+    ms = time_graph(torch, stream, lambda: [ops.matvec_xq(c, xq, y) for c in copies], reps=5)
+    n = len(copies)
+    del copies, base
+    torch.cuda.empty_cache()
+    return ms * 1e3 / n, n, nbytes
+
+
+def matvec_set_bench(torch) -> dict:
+    from rtxllm_amd import formats as F
+
     stream = torch.cuda.Stream()
     per = {}
     for name, fmt, rows, cols, seed in MATVECS:
-        pack = packs.make_pack(fmt, rows, cols, seed)
-        base = ops.DevicePack(pack, dev)
-        nbytes = pack.payload.nbytes + (pack.meta.nbytes if pack.meta is not None else 0)
-        copies = [base]
-        while len(copies) * nbytes < 2 * MALL_BYTES + nbytes:
-            c = ops.DevicePack.__new__(ops.DevicePack)
-            c.fmt, c.rows, c.cols = base.fmt, base.rows, base.cols
-            c.payload = base.payload.clone()
-            c.meta = base.meta.clone() if base.meta is not None else None
-            copies.append(c)
-        xq = ops.stage(ops.to_dev(packs.normal_f32(seed + 0x100, cols), dev))
-        y = torch.empty(rows, dtype=torch.float32, device=dev)
-        ms = time_graph(torch, stream, lambda: [ops.matvec_xq(c, xq, y) for c in copies], reps=5)
-        us = ms * 1e3 / len(copies)
+        us, n, _ = time_matvec(torch, stream, fmt, rows, cols, seed)
         ab = F.algorithmic_bytes(fmt, rows, cols)
         per[name] = {"us": round(us, 3), "GB/s": round(ab / us / 1e3, 1),
-                     "frac": round(ab / us / 1e3 / HBM_PEAK_GBS, 4), "copies": len(copies)}
-        del copies
-        torch.cuda.empty_cache()
+                     "frac": round(ab / us / 1e3 / HBM_PEAK_GBS, 4), "copies": n}
     tot_b = sum(F.algorithmic_bytes(f, r, c) for _, f, r, c, _ in MATVECS)
     tot_us = sum(v["us"] for v in per.values())
     return {"per_matvec": per, "GB/s": round(tot_b / tot_us / 1e3, 1),
             "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+Q4K_LAYOUTS = {"raw": 0, "split-predecoded": 1, "split-half": 2, "split-compact": 3, "split-native": 4,
+               "raw-predecoded": 8}
+Q4K_SWEEP_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336)]
+
+
+def q4k_sweep(torch) -> dict:
+    """Every Q4_K resident layout at the config shapes: us, algorithmic GB/s
+    (144 B per block) and resident bytes; the fastest layout per shape is the
+    MI355X pack policy (rtxllm_amd.manifest.auto_policy)."""
+    from rtxllm_amd import formats as F
+
+    stream = torch.cuda.Stream()
+    out = {}
+    for rows, cols in Q4K_SWEEP_SHAPES:
+        ab = F.algorithmic_bytes(F.Q4K_RAW, rows, cols)
+        row = {}
+        for name, fmt in Q4K_LAYOUTS.items():
+            us, _, nbytes = time_matvec(torch, stream, fmt, rows, cols, 0x5EED0001)
+            row[name] = {"us": round(us, 3), "GB/s": round(ab / us / 1e3, 1), "resident_bytes": int(nbytes)}
+        best = min(row, key=lambda k: row[k]["us"])
+        out[f"{rows}x{cols}"] = {"blocks": rows * cols // 256, "layouts": row, "fastest": best}
+    return out
 
 
 # ---- CPU baseline -------------------------------------------------------------
@@ -408,6 +444,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.traffic_probe:
         traffic_probe(torch)
+        return 0
+    if args.q4k_sweep:
+        print(json.dumps({"q4k_sweep": q4k_sweep(torch)}), flush=True)
         return 0
     dec = decode_bench(torch, args)
     dom = dec["stages"][dec["dominant"]]

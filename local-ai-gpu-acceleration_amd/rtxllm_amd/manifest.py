@@ -32,6 +32,18 @@ Q4K_POLICIES = {
     "split-native": (F.Q4K_SPLIT_NATIVE, "native16"),
 }
 RAW_TYPES = {F.IQ2S: "IQ2_S", F.IQ3S: "IQ3_S", F.Q5K: "Q5_K"}
+
+
+def auto_policy(rows: int, cols: int, lossy: bool = False) -> str:
+    """The Q4_K pack layout for a rows x cols tensor on MI355X, from the layout
+    sweep (bench.py --q4k-sweep, HBM-cold, at 4096x4096, 14336x4096 and
+    4096x14336): split-native (the raw 16-byte head beside the quants) is the
+    fastest exact layout at every shape; split-half (fp16 products, lossy) is
+    4-7 % faster above 65536 blocks and is chosen only when lossy layouts are
+    allowed. The reference's auto policy (q4k_resident_pack.py:75-79: compact
+    up to 4096 blocks, else predecoded) is an RTX 3060 measurement; on MI355X
+    both are slower than split-native."""
+    return "split-half" if lossy and rows * cols // F.BLOCK_VALUES > 65536 else "split-native"
 KERNEL_LABELS = {"IQ2_S": "iq2s_raw_block_probe", "IQ3_S": "iq3s_raw_block_probe", "Q5_K": "q5k_raw_block_probe"}
 
 
@@ -44,6 +56,7 @@ class Tensor:
     rows: int
     cols: int
     blocks: np.ndarray  # uint8, rows * cols / 256 blocks
+    offset: int | None = None  # absolute offset in the source GGUF (else synthetic, in tensor order)
 
 
 def _label(name: str) -> str:
@@ -64,17 +77,20 @@ def _layer_role(name: str) -> tuple[int | None, str]:
 def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-native", write_blocks: bool = True,
                 absolute_paths: bool = False, model: str = "synthetic.gguf") -> dict[str, Path]:
     """Writes the packs; returns the paths of "q4k_manifest", "iq_manifest" and
-    "tensor_plan" (a manifest only when it has tensors)."""
+    "tensor_plan" (a manifest only when it has tensors). policy: a Q4_K split
+    layout, or "auto" / "auto-lossy" for auto_policy() per tensor."""
     out_dir = Path(out_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
-    split_fmt, meta_label = Q4K_POLICIES[policy]
+    if policy not in Q4K_POLICIES and policy not in ("auto", "auto-lossy"):
+        raise ValueError(f"unknown Q4_K policy {policy!r}")
 
     def rel(p: Path) -> str:
         return str(p.resolve() if absolute_paths else p.relative_to(out_dir))
 
-    offset = 4096  # synthetic GGUF data offsets, in tensor order
+    next_offset = 4096  # synthetic GGUF data offsets, in tensor order
     plan, q4k, raw = [], [], []
     for t in tensors:
+        offset = t.offset if t.offset is not None else next_offset
         n_blocks = t.rows * (t.cols // F.BLOCK_VALUES)
         block_bytes = F.GGUF_BLOCK_BYTES[F.Q4K_RAW if t.fmt == F.Q4K_RAW else t.fmt]
         blocks = np.ascontiguousarray(t.blocks, dtype=np.uint8)
@@ -85,6 +101,8 @@ def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-nativ
                      "absolute_offset": offset})
         label = _label(t.name)
         if t.fmt == F.Q4K_RAW:
+            tpolicy = policy if policy in Q4K_POLICIES else auto_policy(t.rows, t.cols, policy == "auto-lossy")
+            split_fmt, meta_label = Q4K_POLICIES[tpolicy]
             payload, meta = packs.q4k_split(split_fmt, blocks)
             pp = out_dir / f"{label}.q4k_payload.bin"
             mp = out_dir / f"{label}.q4k_meta.{meta_label}.bin"
@@ -98,12 +116,12 @@ def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-nativ
             q4k.append({
                 "name": t.name, "dimensions": [t.cols, t.rows], "rows": t.rows, "cols": t.cols,
                 "block_count": n_blocks, "source_offset": offset, "source_bytes": int(blocks.size),
-                "source_checksum": _checksum(blocks), "policy": policy, "metadata_format": meta_label,
+                "source_checksum": _checksum(blocks), "policy": tpolicy, "metadata_format": meta_label,
                 "payload_path": rel(pp), "payload_bytes": int(payload.size), "payload_checksum": _checksum(payload),
                 "metadata_path": rel(mp), "metadata_bytes": int(meta.size), "metadata_checksum": _checksum(meta),
                 "blocks_path": bp, "resident_bytes": int(payload.size + meta.size),
                 "compression_ratio_vs_fp16": (t.rows * t.cols * 2) / float(payload.size + meta.size),
-                "runtime_kernel": policy,
+                "runtime_kernel": tpolicy,
             })
         else:
             pp = out_dir / f"{label}.{gguf_type.lower()}_raw_blocks.bin"
@@ -117,7 +135,7 @@ def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-nativ
                 "payload_checksum": _checksum(blocks), "resident_bytes": int(blocks.size), "policy": "raw-blocks",
                 "runtime_kernel": KERNEL_LABELS[gguf_type],
             })
-        offset += int(blocks.size)
+        next_offset = offset + int(blocks.size)
 
     paths = {"tensor_plan": out_dir / "tensor_plan.json"}
     paths["tensor_plan"].write_text(json.dumps({"model": model, "tensors": plan}, indent=1))

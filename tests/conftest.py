@@ -1,3 +1,5 @@
+import shutil
+import subprocess
 import sys
 from pathlib import Path
 
@@ -28,3 +30,18 @@ def rlib():
     from rtxllm_amd import _lib
 
     return _lib.lib()
+
+
+@pytest.fixture(scope="session")
+def selftest(tmp_path_factory) -> Path:
+    """The native runtime self-test (tests/native/runtime_selftest.cpp with the
+    library's pack-manifest loaders), built here with g++."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path_factory.mktemp("native") / "runtime_selftest"
+    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", "-Werror", "-I", str(REPO / "include"),
+                    str(REPO / "tests" / "native" / "runtime_selftest.cpp"),
+                    str(PKG / "csrc" / "pack_manifest.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, timeout=300)
+    return exe

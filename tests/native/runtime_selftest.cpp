@@ -102,10 +102,13 @@ int load_mode(char** argv) {
   try {
     const std::filesystem::path root = argv[5];
     auto under = [&](const std::filesystem::path& p) { return p.is_absolute() ? p : root / p; };
-    const auto q = load_q4k_manifest(argv[2]);
-    const auto i = load_iq_manifest(argv[3]);
-    validate_q4k_manifest_tensors_against_plan(select_q4k_tensors(q, {}, 0), argv[4]);
-    validate_iq_manifest_tensors_against_plan(i.tensors, argv[4]);
+    // "-" stands for a manifest the packs do not have
+    const bool has_q = std::string(argv[2]) != "-", has_i = std::string(argv[3]) != "-";
+    const auto q = has_q ? load_q4k_manifest(argv[2]) : Q4KManifest{};
+    const auto i = has_i ? load_iq_manifest(argv[3]) : IQManifest{};
+    if (has_q) validate_q4k_manifest_tensors_against_plan(select_q4k_tensors(q, {}, 0), argv[4]);
+    if (has_i) validate_iq_manifest_tensors_against_plan(i.tensors, argv[4]);
+    int bad = 0;
     for (const auto& t : q.tensors) {
       const bool ok = byte_checksum(load_binary_file(under(t.payload_path), t.payload_bytes, "payload")) ==
                           t.payload_checksum &&
@@ -116,18 +119,20 @@ int load_mode(char** argv) {
                            t.source_checksum);
       std::printf("q4k %s layer=%d role=%s rows=%u cols=%u policy=%s ok=%d\n", t.name.c_str(), t.layer,
                   t.role.c_str(), t.rows, t.cols, t.policy.c_str(), ok ? 1 : 0);
+      bad += ok ? 0 : 1;
     }
     for (const auto& t : i.tensors) {
       const bool ok =
           byte_checksum(load_binary_file(under(t.payload_path), t.payload_bytes, "payload")) == t.payload_checksum;
       std::printf("raw %s type=%s layer=%d blocks=%llu ok=%d\n", t.name.c_str(), t.type.c_str(), t.layer,
                   static_cast<unsigned long long>(t.block_count), ok ? 1 : 0);
+      bad += ok ? 0 : 1;
     }
+    return bad == 0 ? 0 : 1;
   } catch (const std::exception& e) {
     std::printf("error %s\n", e.what());
     return 1;
   }
-  return 0;
 }
 
 int main(int argc, char** argv) {

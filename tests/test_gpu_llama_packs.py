@@ -109,3 +109,46 @@ def test_packs_refused_when_incomplete_mislaid_or_corrupt(source, tmp_path):
     with pytest.raises(HipError, match="checksum mismatch: output.weight"):
         m.load_packs(paths["q4k_manifest"], paths["iq_manifest"], tmp_path / "c")
     m.close()
+
+
+def test_gguf_file_loads_bit_identical_and_step_matches(source, tmp_path):
+    """The same model as a GGUF file (quantized tensors + F32 norms + llama.*
+    keys): rtxllm_amd.gguf reads its shape and formats, writes the packs and
+    loads them with the norms into a new model, which matches the source."""
+    from rtxllm_amd import gguf as G
+
+    s = SMALL
+    prepare(source, SEED)
+    meta = [("general.architecture", 8, "llama"), ("llama.embedding_length", 4, s.hidden),
+            ("llama.block_count", 4, s.n_layers), ("llama.attention.head_count", 4, s.n_heads),
+            ("llama.attention.head_count_kv", 4, s.n_kv_heads), ("llama.feed_forward_length", 4, s.ffn),
+            ("llama.rope.freq_base", 6, s.rope_theta), ("llama.attention.layer_norm_rms_epsilon", 6, s.rms_eps)]
+    gtype = {F.IQ3S: "IQ3_S", F.IQ2S: "IQ2_S", F.Q4K_RAW: "Q4_K", F.Q5K: "Q5_K"}
+    tensors = [(t.name, gtype[t.fmt], [t.cols, t.rows], t.blocks) for t in gguf_tensors(source)]
+    H = s.hidden
+    for l in range(s.n_layers):
+        tensors.append((f"blk.{l}.attn_norm.weight", "F32", [H], source.download("attn_norm", np.float32, layer=l)))
+        tensors.append((f"blk.{l}.ffn_norm.weight", "F32", [H], source.download("ffn_norm", np.float32, layer=l)))
+    tensors.append(("output_norm.weight", "F32", [H], source.download("out_norm", np.float32)))
+    path = tmp_path / "small.gguf"
+    G.write(path, meta, tensors)
+    g = G.read(path)
+    fields = G.llama_shape(g)
+    assert np.float32(fields.pop("rms_eps")) == np.float32(s.rms_eps)
+    shape = Shape(**fields, max_ctx=s.max_ctx, page_size=s.page_size)
+    m = Llama(shape, formats=G.model_formats(g))
+    G.load_into(m, g, tmp_path / "packs")
+    for l in range(s.n_layers):
+        for r in WEIGHT_REGIONS + ("attn_norm", "ffn_norm"):
+            assert np.array_equal(m.download(r, np.uint8, layer=l), source.download(r, np.uint8, layer=l)), (l, r)
+        for r in ("k_cache", "v_cache"):
+            m.upload(r, source.download(r, np.uint16, layer=l), layer=l)
+    for r in ("embed", "lm_head", "out_norm"):
+        assert np.array_equal(m.download(r, np.uint8), source.download(r, np.uint8)), r
+    for x in (source, m):
+        x.set_token_pos(99, 120)
+        x.step()
+    torch.cuda.synchronize()
+    assert np.array_equal(m.download("logits", np.float32).view(np.uint32),
+                          source.download("logits", np.float32).view(np.uint32))
+    m.close()

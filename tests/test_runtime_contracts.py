@@ -8,7 +8,6 @@ and byte-sum checksum confirmed."""
 from __future__ import annotations
 
 import json
-import shutil
 import subprocess
 from pathlib import Path
 
@@ -20,19 +19,6 @@ from rtxllm_amd import manifest as M
 from rtxllm_amd import packs
 
 REPO = Path(__file__).resolve().parent.parent
-
-
-@pytest.fixture(scope="module")
-def selftest(tmp_path_factory) -> Path:
-    gxx = shutil.which("g++")
-    if gxx is None:
-        pytest.skip("g++ not available")
-    exe = tmp_path_factory.mktemp("native") / "runtime_selftest"
-    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", "-Werror", "-I", str(REPO / "include"),
-                    str(REPO / "tests" / "native" / "runtime_selftest.cpp"),
-                    str(REPO / "local-ai-gpu-acceleration_amd" / "csrc" / "pack_manifest.cpp"), "-o", str(exe)],
-                   check=True, capture_output=True, timeout=300)
-    return exe
 
 
 def test_native_runtime_selftest(selftest):
@@ -79,7 +65,7 @@ def test_loaders_reject_a_corrupted_pack(selftest, tmp_path):
     f.write_bytes(bytes(b))
     r = subprocess.run([str(selftest), "--load", str(paths["q4k_manifest"]), str(paths["iq_manifest"]),
                         str(paths["tensor_plan"]), str(tmp_path)], capture_output=True, text=True, timeout=120)
-    assert r.returncode == 0
+    assert r.returncode == 1  # a checksum mismatch fails the load
     assert any(l.startswith("raw blk.0.attn_q.weight") and l.endswith("ok=0") for l in r.stdout.splitlines())
     (tmp_path / raw["tensors"][1]["payload_path"]).write_bytes(b"short")
     r = subprocess.run([str(selftest), "--load", str(paths["q4k_manifest"]), str(paths["iq_manifest"]),
