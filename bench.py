@@ -42,12 +42,16 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec-set", action="store_true")
     ap.add_argument("--no-batch8", action="store_true", help="skip the batch-8 decode step")
+    ap.add_argument("--no-read-ceiling", action="store_true", help="skip the streaming-read ceiling per stage size")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 256 MiB device copy and each decode stage of layer 0 a few times (for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), print nothing else")
     ap.add_argument("--q4k-sweep", action="store_true",
                     help="time every Q4_K resident layout at the config shapes (HBM-cold, rotating copies) and "
                          "print the fastest per shape as JSON, nothing else")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time a plain streaming read (rtxllm_stream_read) of each stage's byte count over "
+                         "rotating HBM-cold buffers and print it as JSON, nothing else")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -360,6 +364,42 @@ def q4k_sweep(torch) -> dict:
     return out
 
 
+READ_SIZES = {"o": 7208960, "qkv": 10813440, "attention": 16777216, "iq2s_14336x4096": 18882560,
+              "down": 33030144, "gate_up": 37617664, "lm_head": 361168896}
+
+
+def read_ceiling(torch) -> dict:
+    """What a plain streaming read of the same bytes takes on this GPU
+    (rtxllm_stream_read: 16-byte nontemporal loads, four in flight per lane,
+    the best of four grid sizes), one launch per buffer over rotating buffers
+    spanning more than twice the MALL (HBM-cold), in a hipGraph like the
+    stages."""
+    from rtxllm_amd._lib import check, lib
+
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    out = {}
+    for name, nbytes in READ_SIZES.items():
+        k = max(2, (2 * MALL_BYTES) // nbytes + 1)
+        bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0") for _ in range(k)]
+        res = torch.empty(16384, dtype=torch.int32, device="cuda:0")
+        best = None
+        for grid in (1024, 2048, 4096, 8192):
+            def run(grid=grid):
+                for b in bufs:
+                    check("rtxllm_stream_read", lib().rtxllm_stream_read(b.data_ptr(), nbytes, res.data_ptr(), grid,
+                                                                          sp))
+
+            us = time_graph(torch, stream, run, reps=5) * 1e3 / k
+            best = (us, grid) if best is None or us < best[0] else best
+        us, grid = best
+        out[name] = {"bytes": nbytes, "us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "workgroups": grid}
+        del bufs, res
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---- CPU baseline -------------------------------------------------------------
 
 def cpu_baseline() -> dict:
@@ -445,6 +485,9 @@ def main() -> int:
     if args.traffic_probe:
         traffic_probe(torch)
         return 0
+    if args.read_ceiling:
+        print(json.dumps({"read_ceiling": read_ceiling(torch)}), flush=True)
+        return 0
     if args.q4k_sweep:
         print(json.dumps({"q4k_sweep": q4k_sweep(torch)}), flush=True)
         return 0
@@ -488,6 +531,16 @@ def main() -> int:
                      "cores, f32 accumulate",
             "stages": b8["stages"],
         }
+    if not args.no_read_ceiling:
+        ceil = read_ceiling(torch)
+        out["read_ceiling"] = ceil
+        for st, v in out["stages"].items():
+            if st in ceil and abs(ceil[st]["bytes"] - v["bytes"]) <= 0.02 * v["bytes"]:  # attention: 4096 positions
+                v["read_ceiling_us"] = ceil[st]["us"]
+                v["frac_of_read_ceiling"] = round(ceil[st]["us"] / v["us"], 4)
+        dom_c = ceil.get(dec["dominant"])
+        if dom_c is not None:
+            out["roofline"]["read_ceiling_GBps"] = dom_c["GB/s"]
     if not args.no_matvec_set:
         out["matvec_set"] = matvec_set_bench(torch)
     if not args.no_cpu_baseline:

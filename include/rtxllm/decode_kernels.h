@@ -241,6 +241,13 @@ hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t
                                float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
                                void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Measurement helper, no counterpart in the reference: a plain streaming read
+ * of `bytes` (a multiple of 16, 16-byte aligned) by `workgroups` workgroups of
+ * 256 threads, each writing the xor of what it read to out[workgroup]. bench.py
+ * times it over the decode stages' byte counts as the practical HBM ceiling. */
+hipError_t rtxllm_stream_read(const void* data, size_t bytes, uint32_t* out, uint32_t workgroups,
+                              hipStream_t stream);
+
 /* Host-side helpers (no device work). */
 uint32_t rtxllm_format_payload_block_bytes(int format);
 uint32_t rtxllm_format_meta_block_bytes(int format);

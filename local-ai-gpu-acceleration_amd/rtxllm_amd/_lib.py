@@ -49,6 +49,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
     "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_memory": [_P, _P, _P, _P],
+    "rtxllm_stream_read": [_P, c_size_t, _P, _U, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",
