@@ -38,8 +38,12 @@ namespace rtxllm {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr std::uint32_t kPanel = 512;        // columns per wave
-constexpr std::uint32_t kMaxPanels = 8;      // waves per workgroup
+// 512-column panels measured faster than 256-column ones in 16-wave workgroups
+// (the latter halve B's registers, 4 waves per SIMD instead of 3, but add
+// partials and barrier waits: the batch-8 step lost 6 %).
+constexpr std::uint32_t kPanel = 512;                 // columns per wave
+constexpr int kPanelBlocks = kPanel / 256;            // 256-value blocks per panel
+constexpr std::uint32_t kMaxPanels = 4096 / kPanel;   // waves per workgroup (4096 columns)
 
 constexpr bool fmt_mm_supported(int f) {
   return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S || f == RTXLLM_FMT_Q5K || f == RTXLLM_FMT_Q4K_RAW ||
@@ -321,11 +325,12 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t q = lane >> 4, r16 = lane & 15u;
   const std::uint32_t tiles = (rows + 15u) >> 4;
 
-  // B operands of the panel: 2 blocks x 8 instructions, 1 KB of whole lanes each.
-  const uint4* xb = reinterpret_cast<const uint4*>(x16) + 2u * panel * 8u * 64u + lane;
-  uint4 B[2][8];
+  // B operands of the panel: its blocks x 8 instructions, 1 KB of whole lanes each.
+  constexpr int PB = kPanelBlocks;
+  const uint4* xb = reinterpret_cast<const uint4*>(x16) + PB * panel * 8u * 64u + lane;
+  uint4 B[PB][8];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < PB; ++b)
 #pragma unroll
     for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
 
@@ -333,9 +338,9 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   // b of the panel carry that sequence's block exponent, 2^e[s][b].
   const X16Tail tail = x16_tail(x16, cols);
   const std::uint32_t nb = cols >> 8;
-  float fb[2];
+  float fb[PB];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + 2u * panel + b]);
+  for (int b = 0; b < PB; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + PB * panel + b]);
 
   // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
   // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
@@ -364,18 +369,18 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   }
 
   // (tile, block) units of this wave in order: unit u -> tile blockIdx.x +
-  // (u / 2) * gridDim.x, block 2 panel + u % 2. Loads past the workgroup's
+  // (u / PB) * gridDim.x, block PB panel + u % PB. Loads past the workgroup's
   // last unit re-read that unit (no branch around the loads, so the waits on
   // the ring stay exact counts).
   const std::uint32_t rounds = blockIdx.x < tiles ? (tiles - blockIdx.x + gridDim.x - 1u) / gridDim.x : 0u;
-  const std::uint32_t units = 2u * rounds;
+  const std::uint32_t units = PB * rounds;
   auto load_unit = [&](std::uint32_t u, MmRaw& raw) {
     u = u < units ? u : units - 1u;
-    const std::uint32_t row0 = __builtin_amdgcn_readfirstlane((blockIdx.x + (u >> 1) * gridDim.x) * 16u);
+    const std::uint32_t row0 = __builtin_amdgcn_readfirstlane((blockIdx.x + (u / PB) * gridDim.x) * 16u);
     // the tile's first row in the uniform offset, the lane's row within the
     // tile (clamped to the last row) in the per-lane offset
     const std::uint32_t r = min(r16, rows - 1u - row0);
-    mm_load<FMT>(rsp, rsm, r * prow, r * mrow, row0 * prow, row0 * mrow, 2u * panel + (u & 1u), q, raw);
+    mm_load<FMT>(rsp, rsm, r * prow, r * mrow, row0 * prow, row0 * mrow, PB * panel + (u % PB), q, raw);
   };
   if (units == 0u) {  // whole workgroup: no barrier is left waiting
     epi.finish(wave, lane, nw);
@@ -389,7 +394,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
 
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto finish_unit = [&](std::uint32_t u, const MmRaw& raw) {
-    const int b = static_cast<int>(u & 1u);
+    const int b = static_cast<int>(u % PB);
     f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f}, cm = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -431,15 +436,16 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   };
 
   // unit u sits in ring slot u % NB; PERIOD units bring both the slot and the
-  // block parity back. The main loop's body runs whole (no exit inside it, so
-  // the waits on the ring stay exact counts); the tail runs what is left.
-  constexpr int PERIOD = NB % 2 == 0 ? NB : 2 * NB;
+  // block within the panel back. The main loop's body runs whole (no exit
+  // inside it, so the waits on the ring stay exact counts); the tail runs what
+  // is left.
+  constexpr int PERIOD = NB % PB == 0 ? NB : PB * NB;
   auto step = [&](std::uint32_t u, auto jc) {
     constexpr int j = decltype(jc)::value;
     load_unit(u + NB - 1u, ring[(j + NB - 1) % NB]);
     __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before this unit's work
     finish_unit(u, ring[j % NB]);
-    if constexpr (j % 2 == 1) tile_end(u >> 1);
+    if constexpr (j % PB == PB - 1) tile_end(u / PB);
   };
   std::uint32_t u0 = 0;
   for (; u0 + PERIOD <= units; u0 += PERIOD)
