@@ -43,6 +43,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-matvec-set", action="store_true")
     ap.add_argument("--no-batch8", action="store_true", help="skip the batch-8 decode step")
     ap.add_argument("--no-read-ceiling", action="store_true", help="skip the streaming-read ceiling per stage size")
+    ap.add_argument("--no-context-buckets", action="store_true",
+                    help="skip the short-context decode with a span-bucketed step graph")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run a 256 MiB device copy and each decode stage of layer 0 a few times (for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), print nothing else")
@@ -212,12 +214,49 @@ def decode_bench(torch, args, batch: int = 1) -> dict:
         v["share_of_step"] = round(v["us"] * v["launches_per_step"] / (ms * 1e3), 4)
     dom = max(stages, key=lambda k: stages[k]["us"] * stages[k]["launches_per_step"])
     launches = m.launches_per_step()
+    buckets = None if args.no_context_buckets else context_buckets(torch, m, stream, token, batch, args.steps)
     m.close()
     return {
         "ms_per_step": ms, "tok_s": batch * 1e3 / ms, "wall_s": wall, "step_bytes": step_bytes,
         "GB/s": step_bytes / (ms * 1e-3) / 1e9, "stages": stages, "dominant": dom, "launches": launches,
-        "mean_context": mean_ctx, "tokens_after": tokens,
+        "mean_context": mean_ctx, "tokens_after": tokens, "context_buckets": buckets,
     }
+
+
+SHORT_POS = 64  # a short context: the first step's position
+
+
+def context_buckets(torch, m, stream, token, batch: int, steps: int) -> dict:
+    """Short-context decode: `steps` replays from position SHORT_POS of the
+    full-span step graph against the smallest 128-multiple span graph that
+    holds the last position (its attention launches cover only that span)."""
+    import numpy as np
+
+    sp = stream.cuda_stream
+    span = -(-(SHORT_POS + steps + 1) // 128) * 128
+    m.graph_capture_span(span, sp)
+    assert m.graph_span_for(SHORT_POS + steps - 1) == span
+    out = {"first_pos": SHORT_POS, "steps": steps, "span_positions": span}
+    for name, replay in (("full", lambda: m.graph_replay(sp)), ("span", lambda: m.graph_replay_span(span, sp))):
+        m.set_token_pos(token, [SHORT_POS] * batch if batch > 1 else SHORT_POS)
+        with torch.cuda.stream(stream):
+            replay()  # warm
+            torch.cuda.synchronize()  # the upload below must not race the replay's position update
+            m.set_token_pos(token, [SHORT_POS] * batch if batch > 1 else SHORT_POS)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        assert all(int(p) == SHORT_POS + steps for p in m.download("pos", np.uint32))
+        out[name] = {"ms_per_step": round(ms, 4), "tok_s": round(batch * 1e3 / ms, 1),
+                     "tokens_after": [int(t) for t in m.download("token", np.uint32)]}
+    out["same_tokens"] = out["full"]["tokens_after"] == out["span"]["tokens_after"]
+    out["graph_bytes"] = m.graph_bytes()
+    return out
 
 
 # ---- HBM traffic from counters ------------------------------------------------------
@@ -518,6 +557,8 @@ def main() -> int:
                      "unit": "GB/s", "frac": dom["frac"], "traffic": traffic_of(dec["dominant"]),
                      "algorithmic_bytes": dom["bytes"], "us_per_launch": dom["us"]},
     }
+    if dec["context_buckets"] is not None:
+        out["context_buckets"] = dec["context_buckets"]
     if not args.no_batch8:
         b8 = decode_bench(torch, args, batch=8)
         out["batch8"] = {
@@ -531,6 +572,8 @@ def main() -> int:
                      "cores, f32 accumulate",
             "stages": b8["stages"],
         }
+        if b8["context_buckets"] is not None:
+            out["batch8"]["context_buckets"] = b8["context_buckets"]
     if not args.no_read_ceiling:
         ceil = read_ceiling(torch)
         out["read_ceiling"] = ceil

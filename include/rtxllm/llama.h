@@ -120,6 +120,19 @@ hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream);
 /* Capture one decode step into the model's hipGraph / replay it. */
 hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream);
 hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream);
+/* Context-bucketed step graphs (the reference's graph buckets keyed by query
+ * length, cuda_graph_bucket.h:70-177, and the runner's bucket replay,
+ * main.cpp:4838-4869): a step graph whose attention launches cover only the
+ * first `span` positions (rounded up to whole 128-position chunks), so a short
+ * context does not pay for max_ctx. Capture admits the bucket's graph memory
+ * strictly (hipErrorOutOfMemory); capturing a span again replaces its graph.
+ * Replay is valid while every sequence's position is below span. span_for
+ * returns the smallest captured span above `position` (0: none); graph_bytes
+ * the graph-memory plan over every captured graph. */
+hipError_t rtxllm_llama_graph_capture_span(rtxllm_llama* m, uint32_t span, hipStream_t stream);
+hipError_t rtxllm_llama_graph_replay_span(rtxllm_llama* m, uint32_t span, hipStream_t stream);
+uint32_t rtxllm_llama_graph_span_for(const rtxllm_llama* m, uint32_t position);
+size_t rtxllm_llama_graph_bytes(const rtxllm_llama* m);
 /* One stage of the step alone, on the current state, for per-stage timing (the
  * reference runner's per-phase replay timing, main.cpp:4838-4869): stage 0
  * embedding gather + staging, 1 qkv of `layer`, 2 attention of `layer`, 3 o,

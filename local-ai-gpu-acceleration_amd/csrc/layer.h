@@ -57,11 +57,14 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
 
 // GQA decode attention over positions [0, *pos] of the paged cache: split over
 // context chunks (partials) then combined into att[n_heads * head_dim], which
-// is also staged (16-value groups) into xq_att for the o projection.
+// is also staged (16-value groups) into xq_att for the o projection. The launch
+// covers positions [0, span) (span <= kv.capacity, its chunks only): the
+// position must be below span, positions at or beyond it are not attended.
 hipError_t launch_attention(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream);
-// Per sequence partial-record floats (the batch needs batch times as many).
-std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx);
+                            std::uint32_t span, float* partials, float* att, void* xq_att, hipStream_t stream);
+// Per sequence partial-record floats of a launch over `span` positions (the
+// batch needs batch times as many).
+std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t span);
 // The same for `batch` sequences: sequence s has q16 n_kv * kQ16BytesPerKv
 // bytes on, block-table row s (table_stride entries, >= capacity /
 // page_size), position pos[s], and writes att[s]; xq_att must be null when
@@ -69,7 +72,7 @@ std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv,
 // staged there for the batched o projection (the launch_stage_batch rule;
 // sequences >= batch zero), in the same launch as the combine.
 hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                                  std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
+                                  std::uint32_t span, std::uint32_t batch, std::uint32_t table_stride,
                                   float* partials, float* att, void* xq_att, void* x16_att, hipStream_t stream);
 
 // h += W x (rows % 16 == 0), x either the staged input xq_in or the fp32 x_in

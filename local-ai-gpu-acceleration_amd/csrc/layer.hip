@@ -625,16 +625,16 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
   return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, w.rows, e, stream);
 }
 
-std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t max_ctx) {
-  const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
+std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t span) {
+  const std::uint32_t nchunks = (span + kAttnChunk - 1u) / kAttnChunk;
   return static_cast<std::size_t>(n_kv) * nchunks * (n_heads / n_kv) * (kHeadDim + 2u);
 }
 
 hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                                  std::uint32_t max_ctx, std::uint32_t batch, std::uint32_t table_stride,
+                                  std::uint32_t span, std::uint32_t batch, std::uint32_t table_stride,
                                   float* partials, float* att, void* xq_att, void* x16_att, hipStream_t stream) {
   if (kv.n_kv == 0u || n_heads % kv.n_kv != 0u || n_heads / kv.n_kv > kMaxGroup || kv.capacity == 0u ||
-      kv.capacity > max_ctx || kv.page_size == 0u || kv.capacity % kv.page_size != 0u || batch == 0u ||
+      span == 0u || span > kv.capacity || kv.page_size == 0u || kv.capacity % kv.page_size != 0u || batch == 0u ||
       batch > 65535u || (batch > 1u && (xq_att != nullptr || table_stride < kv.capacity / kv.page_size)))
     return hipErrorInvalidValue;
   if (x16_att != nullptr && (xq_att != nullptr || batch > kBatchMax || (n_heads * kHeadDim) % 256u != 0u))
@@ -642,8 +642,8 @@ hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_
   // element offsets of a layer's K / V cache (every sequence's pages) fit 32 bits
   if (static_cast<std::uint64_t>(kv.capacity) * batch * kv.n_kv * kHeadDim > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const std::uint32_t group = n_heads / kv.n_kv;
-  const std::uint32_t nchunks = (max_ctx + kAttnChunk - 1u) / kAttnChunk;
-  const std::size_t part = attention_partials_floats(n_heads, kv.n_kv, max_ctx);
+  const std::uint32_t nchunks = (span + kAttnChunk - 1u) / kAttnChunk;
+  const std::size_t part = attention_partials_floats(n_heads, kv.n_kv, span);
   if (part > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const std::uint32_t part_stride = static_cast<std::uint32_t>(part), q_stride = kv.n_kv * kQ16PerKv;
   const dim3 grid(nchunks, kv.n_kv, batch), block(64 * kAttnWaves);
@@ -675,9 +675,9 @@ hipError_t launch_attention_batch(const void* q, const KvLayer& kv, std::uint32_
 }
 
 hipError_t launch_attention(const void* q, const KvLayer& kv, std::uint32_t n_heads, const std::uint32_t* pos,
-                            std::uint32_t max_ctx, float* partials, float* att, void* xq_att, hipStream_t stream) {
+                            std::uint32_t span, float* partials, float* att, void* xq_att, hipStream_t stream) {
   if (xq_att == nullptr) return hipErrorInvalidValue;
-  return launch_attention_batch(q, kv, n_heads, pos, max_ctx, 1u, 0u, partials, att, xq_att, nullptr, stream);
+  return launch_attention_batch(q, kv, n_heads, pos, span, 1u, 0u, partials, att, xq_att, nullptr, stream);
 }
 
 hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,

@@ -31,6 +31,11 @@ struct rtxllm_llama {
   rtxllm_llama_config cfg{};
   rtxllm::VramSuperallocator arena;
   rtxllm::HipGraphBucket graph;
+  // context-bucketed step graphs by attention span, and the step's graph
+  // bucket descriptor (admission and graph-memory accounting)
+  std::map<std::uint32_t, rtxllm::HipGraphBucket> span_graphs;
+  rtxllm::HipGraphBucketDescriptor graph_desc;
+  std::uint32_t span = 0;  // positions the attention launches cover: max_ctx, or a bucket's span while capturing
   std::uint32_t q_rows = 0, kv_rows = 0, nslots = 0;
   std::uint32_t key_slots = 0;  // argmax slots of the LM-head launch (per sequence)
   std::size_t partial_floats = 0;  // attention partial records per sequence
@@ -143,6 +148,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   m->nslots = c.hidden / rtxllm::kXGroup;
   m->partial_floats = rtxllm::attention_partials_floats(c.n_heads, c.n_kv_heads, c.max_ctx);
   m->batch = batch;
+  m->span = c.max_ctx;
   m->pages_per_seq = c.max_ctx / c.page_size;
   const std::size_t B = batch;
 
@@ -222,6 +228,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     gd.kernel_launches_per_replay = batch > 1u ? 1u + 9u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
     gd.workspace_high_water_bytes = req.workspace_bytes;
     req.graph_bytes = rtxllm::estimate_hip_graph_bucket_allocation(gd).total_bytes;
+    m->graph_desc = gd;
     std::size_t free_b = 0, total_b = 0;
     const hipError_t mi = hipMemGetInfo(&free_b, &total_b);
     if (mi != hipSuccess) return mi;
@@ -535,7 +542,7 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
                                          m->pages_per_seq, stream);
     }
     case kAttention: {
-      return rtxllm::launch_attention_batch(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx, B,
+      return rtxllm::launch_attention_batch(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, m->span, B,
                                             m->pages_per_seq, region<float>(m, "attn_partials"),
                                             region<float>(m, "att"), nullptr, x16, stream);
     }
@@ -597,7 +604,7 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
                                 stream);
     }
     case kAttention:
-      return rtxllm::launch_attention(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, c.max_ctx,
+      return rtxllm::launch_attention(m->arena.arena_ptr("q"), kv_layer(m, l), c.n_heads, pos, m->span,
                                       region<float>(m, "attn_partials"), region<float>(m, "att"),
                                       m->arena.arena_ptr("xq_att"), stream);
     case kO: {
@@ -687,8 +694,10 @@ extern "C" uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m) {
   return m->batch > 1u ? 1u + 9u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
 }
 
-extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream) {
-  if (m == nullptr || stream == nullptr) return hipErrorInvalidValue;
+namespace {
+
+// Capture one step (attention over m->span positions) into `bucket`.
+hipError_t capture_step(rtxllm_llama* m, rtxllm::HipGraphBucket& bucket, hipStream_t stream) {
   hipError_t st = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
   if (st != hipSuccess) return st;
   const hipError_t launch = rtxllm_llama_step(m, stream);
@@ -700,11 +709,77 @@ extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t st
   }
   if (st != hipSuccess) return st;
   try {
-    m->graph.instantiate(g);
+    bucket.instantiate(g);
   } catch (const std::exception&) {
     return hipErrorInvalidValue;
   }
   return hipSuccess;
+}
+
+rtxllm::HipGraphBucketDescriptor span_descriptor(const rtxllm_llama* m, std::uint32_t span) {
+  rtxllm::HipGraphBucketDescriptor d = m->graph_desc;
+  d.name = "decode_span_" + std::to_string(span);
+  d.query_bucket = span;
+  return d;
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_llama_graph_capture(rtxllm_llama* m, hipStream_t stream) {
+  if (m == nullptr || stream == nullptr) return hipErrorInvalidValue;
+  return capture_step(m, m->graph, stream);
+}
+
+extern "C" hipError_t rtxllm_llama_graph_capture_span(rtxllm_llama* m, uint32_t span, hipStream_t stream) {
+  if (m == nullptr || stream == nullptr || span == 0u || span > m->cfg.max_ctx) return hipErrorInvalidValue;
+  // strict admission of the bucket's graph memory
+  std::size_t free_b = 0, total_b = 0;
+  const hipError_t mi = hipMemGetInfo(&free_b, &total_b);
+  if (mi != hipSuccess) return mi;
+  try {
+    if (rtxllm::estimate_hip_graph_bucket_allocation(span_descriptor(m, span)).total_bytes > free_b)
+      return hipErrorOutOfMemory;
+  } catch (const std::exception&) {
+    return hipErrorInvalidValue;
+  }
+  rtxllm::HipGraphBucket bucket;
+  m->span = span;
+  const hipError_t st = capture_step(m, bucket, stream);
+  m->span = m->cfg.max_ctx;
+  if (st != hipSuccess) return st;
+  m->span_graphs[span] = std::move(bucket);
+  return hipSuccess;
+}
+
+extern "C" hipError_t rtxllm_llama_graph_replay_span(rtxllm_llama* m, uint32_t span, hipStream_t stream) {
+  if (m == nullptr) return hipErrorInvalidValue;
+  const auto it = m->span_graphs.find(span);
+  if (it == m->span_graphs.end()) return hipErrorInvalidValue;
+  try {
+    it->second.replay(stream);
+  } catch (const std::exception&) {
+    return hipErrorLaunchFailure;
+  }
+  return hipSuccess;
+}
+
+extern "C" uint32_t rtxllm_llama_graph_span_for(const rtxllm_llama* m, uint32_t position) {
+  if (m == nullptr) return 0u;
+  const auto it = m->span_graphs.upper_bound(position);
+  return it == m->span_graphs.end() ? 0u : it->first;
+}
+
+extern "C" size_t rtxllm_llama_graph_bytes(const rtxllm_llama* m) {
+  if (m == nullptr) return 0u;
+  std::vector<rtxllm::HipGraphBucketDescriptor> ds;
+  if (m->graph.instantiated()) ds.push_back(m->graph_desc);
+  for (const auto& kv : m->span_graphs) ds.push_back(span_descriptor(m, kv.first));
+  if (ds.empty()) return 0u;
+  try {
+    return rtxllm::build_hip_graph_bucket_plan(ds).total_bytes;
+  } catch (const std::exception&) {
+    return 0u;
+  }
 }
 
 extern "C" hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream) {

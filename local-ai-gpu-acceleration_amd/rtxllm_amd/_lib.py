@@ -46,6 +46,8 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_step": [_P, _S],
     "rtxllm_llama_graph_capture": [_P, _S],
     "rtxllm_llama_graph_replay": [_P, _S],
+    "rtxllm_llama_graph_capture_span": [_P, _U, _S],
+    "rtxllm_llama_graph_replay_span": [_P, _U, _S],
     "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
     "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_memory": [_P, _P, _P, _P],
@@ -80,6 +82,8 @@ _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_llama_destroy": (None, [_P]),
     "rtxllm_llama_region": (_P, [_P, ctypes.c_char_p, _U, _P]),
     "rtxllm_llama_launches_per_step": (c_uint32, [_P]),
+    "rtxllm_llama_graph_span_for": (c_uint32, [_P, _U]),
+    "rtxllm_llama_graph_bytes": (c_size_t, [_P]),
     "rtxllm_q4k_split_pack": (c_int, [c_int, _P, c_size_t, _P, _P]),
     "rtxllm_synth_raw_blocks": (c_int, [c_int, c_uint64, c_size_t, c_float, c_float, _P, c_int]),
     "rtxllm_synth_normal_f32": (c_int, [c_uint64, c_size_t, c_float, c_float, _P, c_int]),

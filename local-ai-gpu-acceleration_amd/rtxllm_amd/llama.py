@@ -135,6 +135,20 @@ class Llama:
     def graph_replay(self, stream: int) -> None:
         check("rtxllm_llama_graph_replay", lib().rtxllm_llama_graph_replay(self.h, stream))
 
+    def graph_capture_span(self, span: int, stream: int) -> None:
+        """Capture a step whose attention covers only positions below `span`."""
+        check("rtxllm_llama_graph_capture_span", lib().rtxllm_llama_graph_capture_span(self.h, span, stream))
+
+    def graph_replay_span(self, span: int, stream: int) -> None:
+        check("rtxllm_llama_graph_replay_span", lib().rtxllm_llama_graph_replay_span(self.h, span, stream))
+
+    def graph_span_for(self, position: int) -> int:
+        """Smallest captured span above `position` (0: none captured)."""
+        return int(lib().rtxllm_llama_graph_span_for(self.h, position))
+
+    def graph_bytes(self) -> int:
+        return int(lib().rtxllm_llama_graph_bytes(self.h))
+
     STAGES = {"embed": 0, "qkv": 1, "attention": 2, "o": 3, "gate_up": 4, "down": 5, "lm_head": 6}
 
     def launch_stage(self, layer: int, stage: str, stream: int = 0) -> None:

@@ -3,8 +3,9 @@ device-generated packs equal the host generator's bytes; one full decode step
 (Q5_K embedding gather, two mixed-quant layers with fused RMSNorm / RoPE / KV
 append / GQA attention / SiLU-gate / residuals, Q5_K LM head, greedy argmax)
 matches the oracle's step within 1e-3 normwise on logits and hidden state, with
-the same token and the same KV-cache writes; a hipGraph replay of the step is
-bit-identical to the eager step. All calls go through the C-ABI."""
+the same token and the same KV-cache writes; a hipGraph replay of the step,
+and of a step captured over a shorter attention span that still holds the
+position, is bit-identical to the eager step. All calls go through the C-ABI."""
 
 from __future__ import annotations
 
@@ -135,6 +136,60 @@ def test_graph_replay_bit_identical_to_eager():
         assert np.array_equal(m.download("logits", np.float32).view(np.uint32), eager_logits.view(np.uint32))
         assert m.download("token", np.uint32)[0] == eager_tok
         assert m.download("pos", np.uint32)[0] == pos + 1
+    m.close()
+
+
+LONG = Shape(hidden=512, n_heads=4, n_kv_heads=2, ffn=1024, vocab=1000, n_layers=2, max_ctx=1024, page_size=16)
+
+
+@pytest.mark.parametrize("pos", [0, 100, 127, 300, 511])
+def test_span_graph_bit_identical_to_full_step(pos):
+    """A step graph captured over a 128- or 512-position span (1 or 4 of the
+    8 attention chunks) gives the full-span eager step's logits, token and KV
+    writes bit for bit while the position is below the span: the chunks it
+    leaves out hold no position of the context."""
+    s, token = LONG, 11
+    m = build(s, pos)
+    k0 = [m.download("k_cache", np.uint16, layer=l) for l in range(s.n_layers)]
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    m.set_token_pos(token, pos)
+    m.step(sp)
+    torch.cuda.synchronize()
+    eager_logits = m.download("logits", np.float32)
+    eager_tok = m.download("token", np.uint32)[0]
+    eager_k = [m.download("k_cache", np.uint16, layer=l) for l in range(s.n_layers)]
+    assert m.graph_span_for(pos) == 0 and m.graph_bytes() == 0
+    for span in (512, 128):
+        m.graph_capture_span(span, sp)
+    m.graph_capture(sp)
+    span = m.graph_span_for(pos)
+    assert span == (128 if pos < 128 else 512)
+    assert m.graph_span_for(512) == 0 and m.graph_bytes() > 0
+    for _ in range(2):
+        for l in range(s.n_layers):
+            m.upload("k_cache", k0[l], layer=l)
+        m.set_token_pos(token, pos)
+        m.graph_replay_span(span, sp)
+        torch.cuda.synchronize()
+        assert np.array_equal(m.download("logits", np.float32).view(np.uint32), eager_logits.view(np.uint32))
+        assert m.download("token", np.uint32)[0] == eager_tok
+        assert m.download("pos", np.uint32)[0] == pos + 1
+        for l in range(s.n_layers):
+            assert np.array_equal(m.download("k_cache", np.uint16, layer=l), eager_k[l])
+    m.close()
+
+
+def test_span_graph_rejects_bad_spans():
+    from rtxllm_amd._lib import HipError
+
+    m = build(SMALL, 0)
+    sp = torch.cuda.Stream().cuda_stream
+    for bad in (0, SMALL.max_ctx + 1):
+        with pytest.raises(HipError):
+            m.graph_capture_span(bad, sp)
+    with pytest.raises(HipError):  # never captured
+        m.graph_replay_span(128, sp)
     m.close()
 
 

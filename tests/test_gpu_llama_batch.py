@@ -151,6 +151,33 @@ def test_batch_graph_replay_bit_identical_to_eager():
     m.close()
 
 
+def test_batch_span_graph_bit_identical_to_full_step():
+    """Batch 8 over a 1024-position cache, positions below 512: the 512-span
+    step graph gives the eager full-span step's logits and tokens bit for bit."""
+    s = Shape(hidden=512, n_heads=4, n_kv_heads=2, ffn=1024, vocab=1000, n_layers=2, max_ctx=1024, page_size=16,
+              batch=B)
+    positions = [0, 37, 200, 255, 16, 15, 100, 511]
+    m = build(s)
+    k0 = [m.download("k_cache", np.uint16, layer=l) for l in range(s.n_layers)]
+    sp = torch.cuda.Stream().cuda_stream
+    m.set_token_pos(TOKENS, positions)
+    m.step(sp)
+    torch.cuda.synchronize()
+    eager_logits = m.download("logits", np.float32)
+    eager_tok = m.download("token", np.uint32)
+    m.graph_capture_span(512, sp)
+    assert m.graph_span_for(max(positions)) == 512
+    for _ in range(2):
+        for l in range(s.n_layers):
+            m.upload("k_cache", k0[l], layer=l)
+        m.set_token_pos(TOKENS, positions)
+        m.graph_replay_span(512, sp)
+        torch.cuda.synchronize()
+        assert np.array_equal(m.download("logits", np.float32).view(np.uint32), eager_logits.view(np.uint32))
+        assert np.array_equal(m.download("token", np.uint32), eager_tok)
+    m.close()
+
+
 def test_batch_regions_and_launch_count(model):
     m, s = model, SMALL_B
     pps = s.max_ctx // s.page_size
