@@ -543,7 +543,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 dot4 (weight codes x 3-digit int8 activation, exact int32 sums) + f32 scales/accumulate",
+        "dtype": "int8 dot4 (weight codes x 2-digit int8 activation, 15-bit per 16-value group, exact int32 sums) + f32 scales/accumulate",
         "data": "synthetic: random-init seeded GGUF packs (splitmix64), norms 1+N(0,0.02), fp16 KV ~ N(0,1)",
         "config": {"workload": "llama-8B-shape decode step: 32 layers (q/k/v/o IQ3_S, gate/up IQ2_S, down Q4_K "
                                "split-native), Q5_K embed + LM head (vocab 128256), GQA 32/8 x 128, "

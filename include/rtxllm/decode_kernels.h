@@ -201,14 +201,14 @@ hipError_t rtxllm_matvec(int format, const uint8_t* payload, const uint8_t* meta
                          uint32_t rows, uint32_t cols, hipStream_t stream);
 
 /* Staged activation ("xq"): x is cut into 16-value groups; each group is kept as
- * 22-bit fixed point X_j = rint(x_j * K / max|x|), K = 127 * 16384 = 2080768,
- * split into three int8 digits X_j = 16384 H_j + 128 M_j + L_j (H in
- * [-127, 127], M in [-64, 64], L in [-64, 63]), plus the group scale
- * s = max|x| / K and the group sum s * sum(X). Layout of one buffer of
- * rtxllm_xq_bytes(cols) bytes: H[cols], M[cols], L[cols] (int8), s[cols/16],
- * sum[cols/16] (f32). The matvec kernels multiply the weight codes with the
- * digits through exact integer dot products, so the staging rounding (relative
- * step 4.8e-7 of the group maximum) is the only deviation from an fp32 product. */
+ * 15-bit fixed point X_j = rint(x_j * K / max|x|), K = 127 * 256 = 32512,
+ * split into two int8 digits X_j = 256 H_j + L_j (H in [-127, 127], L in
+ * [-128, 127]), plus the group scale s = max|x| / K and the group sum
+ * s * sum(X). Layout of one buffer of rtxllm_xq_bytes(cols) bytes: H[cols],
+ * L[cols] (int8), s[cols/16], sum[cols/16] (f32). The matvec kernels multiply
+ * the weight codes with the digits through exact integer dot products, so the
+ * staging rounding (a step of 3.1e-5 of the group maximum) is the only
+ * deviation from an fp32 product. */
 size_t rtxllm_xq_bytes(uint32_t cols);
 /* xq = stage(x * weight) (weight may be null: stage x). cols % 256 == 0. */
 hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t cols, void* xq,

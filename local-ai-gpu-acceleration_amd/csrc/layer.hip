@@ -62,12 +62,11 @@ __device__ __forceinline__ void stage_group16(const XQOut& xq, std::uint32_t g0,
   const float s = m / kXQLimitF;
   int X = static_cast<int>(rintf(x * inv));
   X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
-  int H, M, L;
-  xq_digits(X, H, M, L);
+  int H, L;
+  xq_digits(X, H, L);
   const int total = wave_sum_i(owner ? X : 0);
   if (owner) {
     xq.h[idx] = static_cast<std::int8_t>(H);
-    xq.m[idx] = static_cast<std::int8_t>(M);
     xq.l[idx] = static_cast<std::int8_t>(L);
   }
   if (lane == 0u) {
@@ -476,9 +475,9 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   int X0 = static_cast<int>(rintf(a0 * inv)), X1 = static_cast<int>(rintf(a1 * inv));
   X0 = X0 > kXQLimit ? kXQLimit : (X0 < -kXQLimit ? -kXQLimit : X0);
   X1 = X1 > kXQLimit ? kXQLimit : (X1 < -kXQLimit ? -kXQLimit : X1);
-  int H0, M0, L0, H1, M1, L1;
-  xq_digits(X0, H0, M0, L0);
-  xq_digits(X1, H1, M1, L1);
+  int H0, L0, H1, L1;
+  xq_digits(X0, H0, L0);
+  xq_digits(X1, H1, L1);
   int total = X0 + X1;
   total += __shfl_xor(total, 1, 64);
   total += __shfl_xor(total, 2, 64);
@@ -488,7 +487,6 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
                                       ((static_cast<std::uint32_t>(hi) & 0xFFu) << 8));
   };
   *reinterpret_cast<std::uint16_t*>(xq.h + d0) = pair(H0, H1);
-  *reinterpret_cast<std::uint16_t*>(xq.m + d0) = pair(M0, M1);
   *reinterpret_cast<std::uint16_t*>(xq.l + d0) = pair(L0, L1);
   if ((lane & 7u) == 0u) {
     const std::uint32_t t = d0 / kXGroup;

@@ -3,20 +3,19 @@
 // The matvec kernels multiply small integer weight codes (Q4_K/Q5_K quants,
 // signed IQ grid magnitudes) with the activation through v_dot4_i32_i8. For
 // that the fp32 activation is staged once per 16-value group as fixed point:
-// X_j = rint(x_j * K / max|x|) with K = 127 * 16384 = 2080768, split into three
-// int8 digits X_j = 16384 H_j + 128 M_j + L_j (H in [-127, 127], M in
-// [-64, 64], L in [-64, 63]), with the group scale s = max|x| / K, so that
-// x_j ~= s * X_j (relative step 4.8e-7 of the group maximum, close to fp32's
-// own rounding). The integer dot products are exact; only the staging rounds.
+// X_j = rint(x_j * K / max|x|) with K = 127 * 256 = 32512, split into two int8
+// digits X_j = 256 H_j + L_j (H in [-127, 127], L in [-128, 127]), with the
+// group scale s = max|x| / K, so that x_j ~= s * X_j (a step of 3.1e-5 of the
+// group maximum: 15 bits, finer than fp16's 11-bit mantissa). The integer dot
+// products are exact; only the staging rounds.
 // Every producer (the staging kernel, the kernels' self-staging path, fused
 // epilogues) implements this one rule, so all paths see identical digits.
 //
 // HBM layout of a staged vector of `cols` values (cols % 256 == 0), one
 // allocation of xq_bytes(cols):
 //   [0, cols)               int8 H digits
-//   [cols, 2 cols)          int8 M digits
-//   [2 cols, 3 cols)        int8 L digits
-//   [3 cols, 3 cols + G*4)  f32 group scale s, G = cols / 16
+//   [cols, 2 cols)          int8 L digits
+//   [2 cols, 2 cols + G*4)  f32 group scale s, G = cols / 16
 //   [.., + G*4)             f32 group sum s * sum_j X_j
 #pragma once
 
@@ -25,21 +24,18 @@
 namespace rtxllm {
 
 constexpr int kXGroup = 16;
-constexpr int kXQLimit = 2080768;  // 127 * 16384
-constexpr float kXQLimitF = 2080768.0f;
+constexpr int kXQLimit = 32512;  // 127 * 256
+constexpr float kXQLimitF = 32512.0f;
 
-// X -> (H, M, L) with X = 16384 H + 128 M + L, |X| <= kXQLimit.
-__host__ __device__ inline void xq_digits(int X, int& H, int& M, int& L) {
-  H = (X + 8192) >> 14;
-  const int R = X - 16384 * H;
-  M = (R + 64) >> 7;
-  L = R - 128 * M;
+// X -> (H, L) with X = 256 H + L, |X| <= kXQLimit.
+__host__ __device__ inline void xq_digits(int X, int& H, int& L) {
+  H = (X + 128) >> 8;
+  L = X - 256 * H;
 }
 
 // One staged group in a lane's registers: digit j in byte (j & 3) of word j >> 2.
 struct XG {
   std::uint32_t h[4];
-  std::uint32_t m[4];
   std::uint32_t l[4];
   float s;
   float sum;
@@ -47,7 +43,6 @@ struct XG {
 
 struct XQ {
   const std::int8_t* h;
-  const std::int8_t* m;
   const std::int8_t* l;
   const float* s;
   const float* sum;
@@ -55,31 +50,30 @@ struct XQ {
 
 struct XQOut {
   std::int8_t* h;
-  std::int8_t* m;
   std::int8_t* l;
   float* s;
   float* sum;
 };
 
 __host__ __device__ inline std::size_t xq_bytes(std::uint32_t cols) {
-  return 3u * static_cast<std::size_t>(cols) + 8u * static_cast<std::size_t>(cols / kXGroup);
+  return 2u * static_cast<std::size_t>(cols) + 8u * static_cast<std::size_t>(cols / kXGroup);
 }
 
 __host__ __device__ inline XQ xq_view(const void* base, std::uint32_t cols) {
   const std::int8_t* b = static_cast<const std::int8_t*>(base);
-  const float* s = reinterpret_cast<const float*>(b + 3u * static_cast<std::size_t>(cols));
-  return XQ{b, b + cols, b + 2u * static_cast<std::size_t>(cols), s, s + cols / kXGroup};
+  const float* s = reinterpret_cast<const float*>(b + 2u * static_cast<std::size_t>(cols));
+  return XQ{b, b + cols, s, s + cols / kXGroup};
 }
 
 __host__ __device__ inline XQOut xq_out(void* base, std::uint32_t cols) {
   std::int8_t* b = static_cast<std::int8_t*>(base);
-  float* s = reinterpret_cast<float*>(b + 3u * static_cast<std::size_t>(cols));
-  return XQOut{b, b + cols, b + 2u * static_cast<std::size_t>(cols), s, s + cols / kXGroup};
+  float* s = reinterpret_cast<float*>(b + 2u * static_cast<std::size_t>(cols));
+  return XQOut{b, b + cols, s, s + cols / kXGroup};
 }
 
 __device__ __forceinline__ void xg_zero(XG& g) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) g.h[i] = g.m[i] = g.l[i] = 0u;
+  for (int i = 0; i < 4; ++i) g.h[i] = g.l[i] = 0u;
   g.s = 0.0f;
   g.sum = 0.0f;
 }
@@ -95,20 +89,18 @@ __device__ __forceinline__ void quant16(const float v[16], XG& g) {
   int total = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    std::uint32_t hw = 0u, mw = 0u, lw = 0u;
+    std::uint32_t hw = 0u, lw = 0u;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       int X = static_cast<int>(rintf(v[4 * w + b] * inv));
       X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
-      int H, M, L;
-      xq_digits(X, H, M, L);
+      int H, L;
+      xq_digits(X, H, L);
       hw |= (static_cast<std::uint32_t>(H) & 0xFFu) << (8 * b);
-      mw |= (static_cast<std::uint32_t>(M) & 0xFFu) << (8 * b);
       lw |= (static_cast<std::uint32_t>(L) & 0xFFu) << (8 * b);
       total += X;
     }
     g.h[w] = hw;
-    g.m[w] = mw;
     g.l[w] = lw;
   }
   g.sum = g.s * static_cast<float>(total);
@@ -116,10 +108,8 @@ __device__ __forceinline__ void quant16(const float v[16], XG& g) {
 
 __device__ __forceinline__ void xg_load(const XQ& x, std::uint32_t group, XG& g) {
   const uint4 h = *reinterpret_cast<const uint4*>(x.h + kXGroup * group);
-  const uint4 m = *reinterpret_cast<const uint4*>(x.m + kXGroup * group);
   const uint4 l = *reinterpret_cast<const uint4*>(x.l + kXGroup * group);
   g.h[0] = h.x, g.h[1] = h.y, g.h[2] = h.z, g.h[3] = h.w;
-  g.m[0] = m.x, g.m[1] = m.y, g.m[2] = m.z, g.m[3] = m.w;
   g.l[0] = l.x, g.l[1] = l.y, g.l[2] = l.z, g.l[3] = l.w;
   g.s = x.s[group];
   g.sum = x.sum[group];
@@ -148,17 +138,15 @@ __device__ __forceinline__ void xg_stage(const float* __restrict__ x, const floa
 
 __device__ __forceinline__ void xg_store(const XQOut& x, std::uint32_t group, const XG& g) {
   *reinterpret_cast<uint4*>(x.h + kXGroup * group) = make_uint4(g.h[0], g.h[1], g.h[2], g.h[3]);
-  *reinterpret_cast<uint4*>(x.m + kXGroup * group) = make_uint4(g.m[0], g.m[1], g.m[2], g.m[3]);
   *reinterpret_cast<uint4*>(x.l + kXGroup * group) = make_uint4(g.l[0], g.l[1], g.l[2], g.l[3]);
   x.s[group] = g.s;
   x.sum[group] = g.sum;
 }
 
-// sum_j w_j X_j = 16384 sum w H + 128 sum w M + sum w L, exact in int32 for
-// weights |w| <= 31 (|result| < 16 * 31 * 2^21 < 2^31); two shift-adds.
-__device__ __forceinline__ int dot_digits(int ah, int am, int al) {
-  const std::uint32_t lo = (static_cast<std::uint32_t>(am) << 7) + static_cast<std::uint32_t>(al);
-  return static_cast<int>((static_cast<std::uint32_t>(ah) << 14) + lo);
+// sum_j w_j X_j = 256 sum w H + sum w L, exact in int32 for int8 weights
+// (|result| <= 16 * 128 * 32640 < 2^27); one shift-add.
+__device__ __forceinline__ int dot_digits(int ah, int al) {
+  return static_cast<int>((static_cast<std::uint32_t>(ah) << 8) + static_cast<std::uint32_t>(al));
 }
 
 // a . b over four int8 lanes, starting a chain from 0: the three-operand
@@ -172,14 +160,13 @@ __device__ __forceinline__ int sdot4_0(std::uint32_t a, std::uint32_t b) {
 
 // The dot of 16 int8 weights (4 words) with a staged group.
 __device__ __forceinline__ int dot16(const std::uint32_t w[4], const XG& x) {
-  int ah = sdot4_0(w[0], x.h[0]), am = sdot4_0(w[0], x.m[0]), al = sdot4_0(w[0], x.l[0]);
+  int ah = sdot4_0(w[0], x.h[0]), al = sdot4_0(w[0], x.l[0]);
 #pragma unroll
   for (int i = 1; i < 4; ++i) {
     ah = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.h[i]), ah, false);
-    am = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.m[i]), am, false);
     al = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.l[i]), al, false);
   }
-  return dot_digits(ah, am, al);
+  return dot_digits(ah, al);
 }
 
 }  // namespace rtxllm

@@ -341,9 +341,9 @@ void orc_q4k_split(int fmt, const uint8_t* raw, size_t n_blocks, uint8_t* payloa
   }
 }
 
-void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* m, int8_t* l,
-                          float* scale, float* sum) {
-  const float K = 2080768.0f; /* 127 * 16384 */
+void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* l, float* scale,
+                          float* sum) {
+  const float K = 32512.0f; /* 127 * 256 */
   for (uint32_t g = 0; g < cols / 16u; ++g) {
     float v[16];
     float mx = 0.0f;
@@ -357,13 +357,10 @@ void orc_stage_activation(const float* x, const float* weight, uint32_t cols, in
     int total = 0;
     for (int j = 0; j < 16; ++j) {
       const float r = rintf(v[j] * inv);
-      const int X = isnan(r) ? 0 : (r > K ? 2080768 : (r < -K ? -2080768 : (int)r));
-      const int H = (int)floor((X + 8192) / 16384.0);
-      const int R = X - 16384 * H;
-      const int M = (int)floor((R + 64) / 128.0);
+      const int X = isnan(r) ? 0 : (r > K ? 32512 : (r < -K ? -32512 : (int)r));
+      const int H = (int)floor((X + 128) / 256.0);
       h[16u * g + j] = (int8_t)H;
-      m[16u * g + j] = (int8_t)M;
-      l[16u * g + j] = (int8_t)(R - 128 * M);
+      l[16u * g + j] = (int8_t)(X - 256 * H);
       total += X;
     }
     sum[g] = scale[g] * (float)total;
@@ -373,7 +370,7 @@ void orc_stage_activation(const float* x, const float* weight, uint32_t cols, in
 typedef struct {
   int fmt;
   const uint8_t *payload, *meta;
-  const int8_t *h, *m, *l;
+  const int8_t *h, *l;
   const float* scale;
   uint32_t cols, r0, r1;
   double* y;
@@ -391,7 +388,7 @@ static void* st_worker(void* arg) {
       const uint8_t* mt = blk_ptr(j->meta, mb, bi);
       for (uint32_t v = 0; v < 256u; ++v) {
         const uint32_t c = b * 256u + v;
-        const double X = 16384.0 * j->h[c] + 128.0 * j->m[c] + j->l[c];
+        const double X = 256.0 * j->h[c] + j->l[c];
         acc += (double)orc_dequant_value(j->fmt, p, mt, v) * ((double)j->scale[c / 16u] * X);
       }
     }
@@ -400,16 +397,15 @@ static void* st_worker(void* arg) {
   return NULL;
 }
 
-void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* m,
-                           const int8_t* l, const float* scale, uint32_t rows, uint32_t cols, double* y,
-                           int nthreads) {
+void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* l,
+                           const float* scale, uint32_t rows, uint32_t cols, double* y, int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > 64) nthreads = 64;
   if ((uint32_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
   st_job jobs[64];
   pthread_t th[64];
   for (int t = 0; t < nthreads; ++t) {
-    st_job jb = {fmt, payload, meta, h, m, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
+    st_job jb = {fmt, payload, meta, h, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
                  (uint32_t)((uint64_t)rows * (t + 1) / nthreads), y};
     jobs[t] = jb;
   }

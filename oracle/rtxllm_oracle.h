@@ -64,15 +64,15 @@ void orc_q4k_split(int fmt, const uint8_t* raw_blocks, size_t n_blocks, uint8_t*
 
 /* Activation staging of the product's integer-dot matvec (its own design, no
  * reference counterpart): per 16-value group, m = max|v|, s = m / K with
- * K = 127 * 16384, X = clamp(rint(v * (K / m)), +-K), digits H = floor((X +
- * 8192) / 16384), R = X - 16384 H, M = floor((R + 64) / 128), L = R - 128 M,
- * sum = s * sum(X). v = x * weight when weight is non-null. */
-void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* m,
-                          int8_t* l, float* scale, float* sum);
+ * K = 127 * 256, X = clamp(rint(v * (K / m)), +-K), digits H = floor((X +
+ * 128) / 256), L = X - 256 H, sum = s * sum(X). v = x * weight when weight is
+ * non-null. */
+void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* l,
+                          float* scale, float* sum);
 /* y = W x_hat with x_hat = s * X (the staged activation), accumulated in double. */
 void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h,
-                           const int8_t* m, const int8_t* l, const float* scale, uint32_t rows,
-                           uint32_t cols, double* y, int nthreads);
+                           const int8_t* l, const float* scale, uint32_t rows, uint32_t cols, double* y,
+                           int nthreads);
 
 /* Greedy token: lowest index among the maxima; start (-FLT_MAX, 0). */
 uint32_t orc_argmax(const float* y, uint32_t n);

@@ -146,7 +146,8 @@ def check_decode(orc, name, pack, rows_limit=None):
     assert rel_err(got_l, ref_l) <= TOL
     assert np.max(np.abs(got_kv - ref_kv)) <= TOL * np.max(np.abs(ref_l))
     assert (got_kv != 0).sum() == (ref_kv != 0).sum()
-    assert got_t == ref_t or abs(float(ref_l[(got_t - token0 - 1) % 32000]) - float(ref_l.max())) <= 1e-5 * abs(
+    # a different token only at a near-tie, inside the staging's error (~2e-5 of the maximum)
+    assert got_t == ref_t or abs(float(ref_l[(got_t - token0 - 1) % 32000]) - float(ref_l.max())) <= 1e-4 * abs(
         float(ref_l.max()))
 
 
@@ -227,6 +228,7 @@ def test_matvec_xq_equals_self_staging_and_staged_oracle(orc, fmt, shape):
     ref = orc.matvec_staged_f64(of, pl, mt, x, rows, cols, 8)
     # same staged digits: only fp32 rounding of the per-group products separates them
     assert np.max(np.abs(y_xq - ref)) / np.max(np.abs(ref)) < 1e-5
-    # and the staged product is an fp32-grade matvec: close to the float64 oracle on the raw x
+    # and the 15-bit staging (a step of 3.1e-5 of each group's maximum) keeps the
+    # product within 1e-4 of the float64 oracle on the raw x (measured ~2e-5)
     ref64 = orc.matvec_f64(of, pl, mt, x, rows, cols, 8)
-    assert np.max(np.abs(y_xq - ref64)) / np.max(np.abs(ref64)) < 2e-5
+    assert np.max(np.abs(y_xq - ref64)) / np.max(np.abs(ref64)) < 1e-4
