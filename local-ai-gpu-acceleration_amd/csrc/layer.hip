@@ -177,16 +177,28 @@ struct EpiResidual {
   const float* w_next;
   XQOut xq;
   float* sumsq;
-  __device__ __forceinline__ void init(std::uint32_t) {}
+  // h and w_next of the workgroup's first group (group blockIdx.x), read at
+  // the kernel's start so that its epilogue waits on no load
+  std::uint32_t pf_row0;
+  float pf_h, pf_w;
+  __device__ __forceinline__ void init(std::uint32_t lane) {
+    pf_row0 = blockIdx.x * kXGroup;
+    const std::uint32_t row = pf_row0 + (lane < kXGroup ? lane : 0u);
+    pf_h = h[row];
+    pf_w = w_next != nullptr ? w_next[row] : 1.0f;
+  }
   __device__ __forceinline__ void group(std::uint32_t row0, const float* vals, std::uint32_t lane,
                                         std::uint32_t) const {
     const bool owner = lane < kXGroup;
     const std::uint32_t row = row0 + (owner ? lane : 0u);
-    const float hn = h[row] + (owner ? vals[lane] : 0.0f);
+    const bool pf = row0 == pf_row0;
+    const float h0 = pf ? pf_h : h[row];
+    const float wn = pf ? pf_w : (w_next != nullptr ? w_next[row] : 1.0f);
+    const float hn = h0 + (owner ? vals[lane] : 0.0f);
     if (owner) h[row] = hn;
     const float sq = wave_sum(owner ? hn * hn : 0.0f);
-    // stage the 16-value group h * w_next
-    const float x = owner ? (w_next != nullptr ? hn * w_next[row] : hn) : 0.0f;
+    // stage the 16-value group h * w_next (w_next null: h itself, times 1)
+    const float x = owner ? hn * wn : 0.0f;
     stage_group16(xq, row0, row, x, owner, lane);
     if (lane == 0u) sumsq[row0 / kXGroup] = sq;
   }
@@ -612,7 +624,8 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
                       const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
                       std::uint32_t rope_positions, const std::uint32_t* pos, void* q_out, const KvLayer& kv,
                       hipStream_t stream) {
-  if (rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || q_rows % (kHeadDim * kv.n_kv) != 0u)
+  if (rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || kv.page_size == 0u ||
+      q_rows % (kHeadDim * kv.n_kv) != 0u)
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
   EpiQkv e{};
