@@ -248,6 +248,17 @@ hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t
 hipError_t rtxllm_stream_read(const void* data, size_t bytes, uint32_t* out, uint32_t workgroups,
                               hipStream_t stream);
 
+/* GGUF IQ2_S blocks (format 6) of a rows x cols tensor -> the same bytes in the
+ * IQ2S_UNITS layout (format 9), device to device: per 32-value unit k of block b
+ * of N blocks, qs[4k..4k+3] and signs[4k..4k+3] at 64 b + 8 k, (qh[k],
+ * scales[k]) at 64 N + 16 b + 2 k, and the block's d at 80 N + 2 b. A matvec
+ * then reads three aligned fields per unit instead of five. No counterpart in
+ * the reference (its IQ packs keep the GGUF blocks, iq_resident_pack.py:115-147);
+ * the decode runner keeps a unit copy of IQ2_S gate/up weights at batch 1. out
+ * is 16-byte aligned and rows * cols / 256 * 82 bytes. */
+hipError_t rtxllm_iq2s_units_pack(const uint8_t* raw, uint32_t rows, uint32_t cols, uint8_t* out,
+                                  hipStream_t stream);
+
 /* Host-side helpers (no device work). */
 uint32_t rtxllm_format_payload_block_bytes(int format);
 uint32_t rtxllm_format_meta_block_bytes(int format);

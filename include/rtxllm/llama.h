@@ -73,8 +73,17 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * block_table is [B][max_ctx / page_size] (initially sequence s owns pages
  * [s * max_ctx / page_size, (s + 1) * max_ctx / page_size)).
  * Row layouts: qkv = q rows (n_heads*128) | k rows | v rows; gate_up rows
- * interleaved (2i = gate_i, 2i+1 = up_i). */
+ * interleaved (2i = gate_i, 2i+1 = up_i).
+ * Batch 1 with IQ2_S gate/up also holds "gate_up_units" per layer: the gate/up
+ * weights regrouped into the IQ2S_UNITS layout (rtxllm_iq2s_units_pack), which
+ * its matvec reads. The runner rebuilds a layer's copy before its next launch
+ * after rtxllm_llama_upload of that layer's "gate_up", rtxllm_llama_load_packs
+ * or rtxllm_llama_synth_weights; after writing "gate_up" through a region
+ * pointer, call rtxllm_llama_weights_changed. */
 void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes);
+/* The weights were written through region pointers: rebuild the derived unit
+ * copies before the next launch (no counterpart in the reference). */
+void rtxllm_llama_weights_changed(rtxllm_llama* m);
 
 /* Synchronous host <-> region copies (setup and inspection; not capture-safe):
  * `bytes` at byte `offset` of the region. hipErrorInvalidValue if out of range. */

@@ -18,7 +18,7 @@ bool aligned(const void* p, std::uintptr_t a) { return (reinterpret_cast<std::ui
 // the Q4_K metadata records; reject pointers that break those alignments.
 bool pointers_ok(int fmt, const void* payload, const void* meta, const void* x) {
   if (x != nullptr && !aligned(x, 16)) return false;
-  const bool iq = fmt == RTXLLM_FMT_IQ2S || fmt == RTXLLM_FMT_IQ3S;
+  const bool iq = fmt == RTXLLM_FMT_IQ2S || fmt == RTXLLM_FMT_IQ3S;  // IQ2S_UNITS: 16 (8-byte field loads)
   if (!aligned(payload, iq ? 2 : 16)) return false;
   if (needs_meta(fmt)) {
     const std::uintptr_t ma = fmt == RTXLLM_FMT_Q4K_SPLIT_HALF ? 8 : fmt == RTXLLM_FMT_Q4K_SPLIT_COMPACT ? 4 : 16;
@@ -41,6 +41,28 @@ __global__ __launch_bounds__(256) void dequant_kernel(const std::uint8_t* __rest
   const std::uint8_t* p = payload + blk * rtxllm_format_payload_bytes(FMT);
   const std::uint8_t* m = meta ? meta + blk * rtxllm_format_meta_bytes(FMT) : nullptr;
   out[row * cols + b * 256u + threadIdx.x] = dequant_value<FMT>(p, m, threadIdx.x);
+}
+
+// IQ2S_UNITS: the workgroup gathers its block's 82 bytes back into the GGUF
+// order in LDS, then dequantises them exactly as IQ2_S.
+__global__ __launch_bounds__(256) void dequant_iq2s_units_kernel(const std::uint8_t* __restrict__ payload,
+                                                                 std::uint32_t cols, std::size_t nb,
+                                                                 float* __restrict__ out) {
+  __shared__ std::uint8_t blk[84];
+  const std::size_t b = blockIdx.x;
+  const std::uint32_t bpr = cols >> 8, i = threadIdx.x;
+  if (i < 82u) blk[i] = payload[iq2s_units_offset(b, i, nb)];
+  __syncthreads();
+  out[(b / bpr) * cols + (b % bpr) * 256u + i] = dequant_value<RTXLLM_FMT_IQ2S>(blk, nullptr, i);
+}
+
+// One thread per block: GGUF IQ2_S bytes -> the unit layout.
+__global__ __launch_bounds__(256) void iq2s_units_pack_kernel(const std::uint8_t* __restrict__ raw, std::size_t nb,
+                                                              std::uint8_t* __restrict__ out) {
+  const std::size_t b = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= nb) return;
+  const std::uint8_t* src = raw + 82u * b;
+  for (std::uint32_t i = 0; i < 82u; ++i) out[iq2s_units_offset(b, i, nb)] = src[i];
 }
 
 template <int FMT>
@@ -93,10 +115,26 @@ extern "C" hipError_t rtxllm_dequant_f32(int format, const std::uint8_t* payload
     case RTXLLM_FMT_Q5K: return launch_dequant_fmt<RTXLLM_FMT_Q5K>(payload, meta, rows, cols, out, stream);
     case RTXLLM_FMT_IQ2S: return launch_dequant_fmt<RTXLLM_FMT_IQ2S>(payload, meta, rows, cols, out, stream);
     case RTXLLM_FMT_IQ3S: return launch_dequant_fmt<RTXLLM_FMT_IQ3S>(payload, meta, rows, cols, out, stream);
+    case RTXLLM_FMT_IQ2S_UNITS: {
+      const std::size_t nb = static_cast<std::size_t>(rows) * (cols / 256u);
+      hipLaunchKernelGGL(dequant_iq2s_units_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, payload,
+                         cols, nb, out);
+      return hipGetLastError();
+    }
     case RTXLLM_FMT_Q4K_RAW_PREDECODED:
       return launch_dequant_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED>(payload, meta, rows, cols, out, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+extern "C" hipError_t rtxllm_iq2s_units_pack(const std::uint8_t* raw, std::uint32_t rows, std::uint32_t cols,
+                                             std::uint8_t* out, hipStream_t stream) {
+  if (!shape_ok(rows, cols) || raw == nullptr || out == nullptr || !aligned(out, 16)) return hipErrorInvalidValue;
+  const std::size_t nb = static_cast<std::size_t>(rows) * (cols / 256u);
+  if (nb * 82u > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(iq2s_units_pack_kernel, dim3(static_cast<unsigned>((nb + 255u) / 256u)), dim3(256), 0, stream, raw,
+                     nb, out);
+  return hipGetLastError();
 }
 
 extern "C" hipError_t rtxllm_matvec(int format, const std::uint8_t* payload, const std::uint8_t* meta,

@@ -46,6 +46,11 @@ struct rtxllm_llama {
   // (output phase: LM head + argmax)
   rtxllm::LayerExecutionPlan layer_plan, head_plan;
   rtxllm::AdmissionDecision admission;
+  // Batch 1 with IQ2_S gate/up: the matvec reads a copy in the IQ2S_UNITS
+  // layout ("gate_up_units"), rebuilt from "gate_up" before the next launch
+  // after the layer's weights change (upload, synthesis, packs).
+  bool units = false;
+  std::vector<char> units_dirty;
 };
 
 namespace {
@@ -56,8 +61,9 @@ std::size_t blocks_of(std::uint32_t rows, std::uint32_t cols) {
   return static_cast<std::size_t>(rows) * (cols / 256u);
 }
 
+// Configurable tensor formats (the unit layout is the runner's own copy).
 bool format_ok(int fmt) {
-  return fmt >= RTXLLM_FMT_Q4K_RAW && fmt < RTXLLM_FMT_COUNT;
+  return fmt >= RTXLLM_FMT_Q4K_RAW && fmt < RTXLLM_FMT_COUNT && fmt != RTXLLM_FMT_IQ2S_UNITS;
 }
 
 std::string layer_name(const char* role, std::uint32_t layer) {
@@ -98,6 +104,25 @@ rtxllm::KvLayer kv_layer(const rtxllm_llama* m, std::uint32_t layer) {
   kv.n_kv = m->cfg.n_kv_heads;
   kv.capacity = m->cfg.max_ctx;  // per sequence
   return kv;
+}
+
+void mark_units_dirty(rtxllm_llama* m) {
+  std::fill(m->units_dirty.begin(), m->units_dirty.end(), 1);
+}
+
+// Rebuild the unit copies of the layers whose gate/up weights changed (stream
+// ordered after the writes; a device-to-device regrouping, no allocation).
+hipError_t ensure_units(rtxllm_llama* m, hipStream_t stream) {
+  if (!m->units) return hipSuccess;
+  for (std::uint32_t l = 0; l < m->cfg.n_layers; ++l) {
+    if (!m->units_dirty[l]) continue;
+    const hipError_t st = rtxllm_iq2s_units_pack(
+        static_cast<const std::uint8_t*>(m->arena.arena_ptr(layer_name("gate_up", l))), 2u * m->cfg.ffn,
+        m->cfg.hidden, static_cast<std::uint8_t*>(m->arena.arena_ptr(layer_name("gate_up_units", l))), stream);
+    if (st != hipSuccess) return st;
+    m->units_dirty[l] = 0;
+  }
+  return hipSuccess;
 }
 
 hipError_t synth_tensor(rtxllm_llama* m, const std::string& name, int fmt, std::uint32_t rows, std::uint32_t cols,
@@ -149,6 +174,8 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   m->partial_floats = rtxllm::attention_partials_floats(c.n_heads, c.n_kv_heads, c.max_ctx);
   m->batch = batch;
   m->span = c.max_ctx;
+  m->units = batch == 1u && c.fmt_gate_up == RTXLLM_FMT_IQ2S;
+  m->units_dirty.assign(m->units ? c.n_layers : 0u, 1);
   m->pages_per_seq = c.max_ctx / c.page_size;
   const std::size_t B = batch;
 
@@ -159,6 +186,8 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     add_tensor(specs, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden);
     add_tensor(specs, layer_name("o", l), c.fmt_o, c.hidden, m->q_rows);
     add_tensor(specs, layer_name("gate_up", l), c.fmt_gate_up, 2u * c.ffn, c.hidden);
+    if (batch == 1u && c.fmt_gate_up == RTXLLM_FMT_IQ2S)
+      add_tensor(specs, layer_name("gate_up_units", l), RTXLLM_FMT_IQ2S_UNITS, 2u * c.ffn, c.hidden);
     add_tensor(specs, layer_name("down", l), c.fmt_down, c.hidden, c.ffn);
     specs.push_back({layer_name("attn_norm", l), 4u * c.hidden});
     specs.push_back({layer_name("ffn_norm", l), 4u * c.hidden});
@@ -289,7 +318,7 @@ extern "C" void rtxllm_llama_destroy(rtxllm_llama* m) { delete m; }
 
 extern "C" void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes) {
   if (m == nullptr || name == nullptr) return nullptr;
-  static const char* kPerLayer[] = {"qkv", "qkv_meta", "o", "o_meta", "gate_up", "gate_up_meta", "down",
+  static const char* kPerLayer[] = {"qkv", "qkv_meta", "o", "o_meta", "gate_up", "gate_up_meta", "gate_up_units", "down",
                                     "down_meta", "attn_norm", "ffn_norm", "k_cache", "v_cache", "block_table"};
   std::string key = name;
   for (const char* p : kPerLayer)
@@ -309,6 +338,7 @@ extern "C" hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uin
   std::size_t size = 0;
   auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
   if (base == nullptr || src == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
+  if (m->units && std::strcmp(name, "gate_up") == 0) m->units_dirty[layer] = 1;
   return hipMemcpy(base + offset, src, bytes, hipMemcpyHostToDevice);
 }
 
@@ -445,6 +475,7 @@ extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_m
       if (dst == nullptr || size != bytes.size()) throw std::runtime_error("region size mismatch: " + region);
       const hipError_t st = hipMemcpy(dst, bytes.data(), bytes.size(), hipMemcpyHostToDevice);
       if (st != hipSuccess) throw std::runtime_error(std::string("upload failed: ") + hipGetErrorString(st));
+      mark_units_dirty(m);
     };
     // stack rows (q | k | v) or interleave them (gate_i, up_i) stream by stream
     auto stack = [](std::initializer_list<const std::vector<std::uint8_t>*> parts) {
@@ -498,8 +529,13 @@ extern "C" hipError_t rtxllm_llama_memory(const rtxllm_llama* m, size_t* require
   return hipSuccess;
 }
 
+extern "C" void rtxllm_llama_weights_changed(rtxllm_llama* m) {
+  if (m != nullptr) mark_units_dirty(m);
+}
+
 extern "C" hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_t stream) {
   if (m == nullptr) return hipErrorInvalidValue;
+  mark_units_dirty(m);
   const rtxllm_llama_config& c = m->cfg;
   hipError_t st = hipSuccess;
   for (std::uint32_t l = 0; l < c.n_layers && st == hipSuccess; ++l) {
@@ -614,9 +650,9 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
                                      region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
     }
     case kGateUp: {
-      const TensorRef t = tensor(m, layer_name("gate_up", l));
-      return rtxllm::launch_gate_up(c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn, c.hidden, in,
-                                    region<float>(m, "act"), stream);
+      const TensorRef t = tensor(m, layer_name(m->units ? "gate_up_units" : "gate_up", l));
+      return rtxllm::launch_gate_up(m->units ? RTXLLM_FMT_IQ2S_UNITS : c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn,
+                                    c.hidden, in, region<float>(m, "act"), stream);
     }
     case kDown: {
       const TensorRef t = tensor(m, layer_name("down", l));
@@ -643,7 +679,8 @@ extern "C" hipError_t rtxllm_llama_forward(rtxllm_llama* m, uint32_t first, uint
   if (m == nullptr || first > last || last > m->cfg.n_layers) return hipErrorInvalidValue;
   const float* out_norm = region<float>(m, "out_norm");
   const float* first_norm = first < last ? region<float>(m, layer_name("attn_norm", first)) : out_norm;
-  hipError_t st = launch_stage(m, 0u, kEmbed, (flags & RTXLLM_LLAMA_EMBED) != 0, first_norm, stream);
+  hipError_t st = ensure_units(m, stream);
+  if (st == hipSuccess) st = launch_stage(m, 0u, kEmbed, (flags & RTXLLM_LLAMA_EMBED) != 0, first_norm, stream);
   // Each layer replays the layer plan by phase: stage i of the plan is one of
   // qkv (with the attention over the updated cache), o, gate/up, down (their
   // activation hand-off is fused into the stages, so no feedback launches).
@@ -680,6 +717,8 @@ extern "C" hipError_t rtxllm_llama_launch_stage(rtxllm_llama* m, uint32_t layer,
   const float* next_norm = layer + 1u < m->cfg.n_layers ? region<float>(m, layer_name("attn_norm", layer + 1u))
                                                         : region<float>(m, "out_norm");
   if (stage == kEmbed) next_norm = region<float>(m, layer_name("attn_norm", 0u));
+  const hipError_t st = ensure_units(m, stream);
+  if (st != hipSuccess) return st;
   return launch_stage(m, layer, stage, stage == kEmbed, next_norm, stream);
 }
 
@@ -698,7 +737,9 @@ namespace {
 
 // Capture one step (attention over m->span positions) into `bucket`.
 hipError_t capture_step(rtxllm_llama* m, rtxllm::HipGraphBucket& bucket, hipStream_t stream) {
-  hipError_t st = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+  hipError_t st = ensure_units(m, stream);  // before the capture: the graph holds the step alone
+  if (st != hipSuccess) return st;
+  st = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
   if (st != hipSuccess) return st;
   const hipError_t launch = rtxllm_llama_step(m, stream);
   hipGraph_t g = nullptr;
@@ -755,6 +796,8 @@ extern "C" hipError_t rtxllm_llama_graph_replay_span(rtxllm_llama* m, uint32_t s
   if (m == nullptr) return hipErrorInvalidValue;
   const auto it = m->span_graphs.find(span);
   if (it == m->span_graphs.end()) return hipErrorInvalidValue;
+  const hipError_t st = ensure_units(m, stream);
+  if (st != hipSuccess) return st;
   try {
     it->second.replay(stream);
   } catch (const std::exception&) {
@@ -784,6 +827,8 @@ extern "C" size_t rtxllm_llama_graph_bytes(const rtxllm_llama* m) {
 
 extern "C" hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t stream) {
   if (m == nullptr || !m->graph.instantiated()) return hipErrorInvalidValue;
+  const hipError_t st = ensure_units(m, stream);
+  if (st != hipSuccess) return st;
   try {
     m->graph.replay(stream);
   } catch (const std::exception&) {

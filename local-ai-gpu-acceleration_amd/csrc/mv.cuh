@@ -55,7 +55,9 @@ struct XSrc {
 // same cache lines, which only the L1 turns into one L2 request per line, so
 // those loads keep the default policy.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S; }
+constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S || f == RTXLLM_FMT_IQ2S_UNITS; }
+// IQ2_S values in either layout (same codebooks, same arithmetic).
+constexpr bool fmt_is_iq2s(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ2S_UNITS; }
 template <int FMT>
 constexpr int load_policy() {
   return (fmt_is_iq(FMT) || FMT == RTXLLM_FMT_Q5K) ? 0 : 2;  // 2 = nt
@@ -110,7 +112,7 @@ struct IqLds3 {
   uint4 sign[256];
 };
 template <int FMT>
-using IqLds = typename std::conditional<FMT == RTXLLM_FMT_IQ2S, IqLds2, IqLds3>::type;
+using IqLds = typename std::conditional<fmt_is_iq2s(FMT), IqLds2, IqLds3>::type;
 
 // The same tables as device-global images, built at compile time, in the LDS
 // layout: a workgroup copies its image with direct global -> LDS loads.
@@ -175,8 +177,8 @@ __device__ __forceinline__ void iq_lds_fetch(IqLds<FMT>& t, std::uint32_t wave, 
   constexpr std::uint32_t kChunks = sizeof(IqLds<FMT>) / 1024u;  // 1 KB per wave instruction
   static_assert(sizeof(IqLds<FMT>) % 1024u == 0u, "whole wave chunks");
   const std::uint32_t nw = blockDim.x >> 6;
-  const uint4* src = reinterpret_cast<const uint4*>(FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kIq2sImage)
-                                                                           : static_cast<const void*>(&kIq3sImage));
+  const uint4* src = reinterpret_cast<const uint4*>(fmt_is_iq2s(FMT) ? static_cast<const void*>(&kIq2sImage)
+                                                                      : static_cast<const void*>(&kIq3sImage));
   uint4* dst = reinterpret_cast<uint4*>(&t);
   for (std::uint32_t c = wave; c < kChunks; c += nw)
     __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
@@ -203,7 +205,7 @@ template <int FMT>
 struct FmtBytes {
   // Bytes per block in the payload stream and the metadata stream.
   static constexpr std::uint32_t payload = FMT == RTXLLM_FMT_Q5K ? 176u
-                                           : FMT == RTXLLM_FMT_IQ2S ? 82u
+                                           : fmt_is_iq2s(FMT) ? 82u
                                            : FMT == RTXLLM_FMT_IQ3S ? 110u
                                            : fmt_is_raw_q4k(FMT) ? 144u : 128u;
   static constexpr std::uint32_t meta = FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED ? 64u
@@ -212,12 +214,28 @@ struct FmtBytes {
                                         : FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE ? 16u : 0u;
 };
 
+// Byte i (GGUF order: d, qs[32], signs[32], qh[8], scales[8]) of block b of an
+// IQ2S_UNITS tensor of nb blocks.
+__host__ __device__ inline std::size_t iq2s_units_offset(std::size_t b, std::uint32_t i, std::size_t nb) {
+  if (i < 2u) return 80u * nb + 2u * b + i;                             // d
+  if (i < 34u) return 64u * b + 8u * ((i - 2u) >> 2) + ((i - 2u) & 3u);  // qs
+  if (i < 66u) return 64u * b + 8u * ((i - 34u) >> 2) + 4u + ((i - 34u) & 3u);  // signs
+  if (i < 74u) return 64u * nb + 16u * b + 2u * (i - 66u);              // qh
+  return 64u * nb + 16u * b + 2u * (i - 74u) + 1u;                      // scales
+}
+
+// nb: blocks in the tensor (the unit layout's field streams start at 64 nb and
+// 80 nb); the IQ2S_UNITS offsets are relative to the row's first block.
 template <int FMT>
-__device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k) {
+__device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k, std::uint32_t nb) {
   UnitOff u{};
   const std::uint32_t pb = b * FmtBytes<FMT>::payload, mb = b * FmtBytes<FMT>::meta, g = k >> 1;
   u.g = g;
-  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+  if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
+    u.o[0] = 64u * b + 8u * k;             // qs, signs of the unit
+    u.o[1] = 64u * nb + 16u * b + 2u * k;  // qh, scales of the unit
+    u.o[2] = 80u * nb + 2u * b;            // d
+  } else if constexpr (fmt_is_iq2s(FMT)) {
     u.o[0] = pb;                 // d
     u.o[1] = pb + 2u + 4u * k;   // qs (grid low bytes)
     u.o[2] = pb + 34u + 4u * k;  // sign bytes
@@ -269,7 +287,8 @@ __device__ __forceinline__ void unit_groups(std::uint32_t b, std::uint32_t k, st
   }
 }
 
-// rp / rm: this row's start in the payload / metadata stream (wave-uniform).
+// rp / rm: this row's start in the payload / metadata stream (wave-uniform);
+// IQ2S_UNITS: sp = blocks before this row.
 template <int FMT>
 __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, const UnitOff& u,
                                           UnitRaw& r) {
@@ -281,7 +300,13 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z, r.a[3] = q.w;
     r.b[0] = h.x, r.b[1] = h.y, r.b[2] = h.z, r.b[3] = h.w;
     r.c[0] = qh.x, r.c[1] = qh.y, r.c[2] = qh.z, r.c[3] = qh.w;
-  } else if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+  } else if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
+    const u32x2 q = bld_u64<P>(rp, u.o[0], 64u * sp);
+    r.a[0] = q.x, r.a[1] = q.y;
+    const std::uint32_t hs = bld_u16<P>(rp, u.o[1], 16u * sp);
+    r.c[1] = hs & 0xFFu, r.c[2] = hs >> 8;
+    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
+  } else if constexpr (fmt_is_iq2s(FMT)) {
     r.c[0] = bld_u16<P>(rp, u.o[0], sp);
     r.a[0] = bld_u32<P>(rp, u.o[1], sp);
     r.a[1] = bld_u32<P>(rp, u.o[2], sp);
@@ -345,7 +370,7 @@ struct IqWords {
 
 template <int FMT>
 __device__ __forceinline__ void unit_lookup(const UnitRaw& r, const IqLds<FMT>* t, IqWords& q) {
-  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+  if constexpr (fmt_is_iq2s(FMT)) {
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
@@ -405,7 +430,7 @@ __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, con
   const float d = h2f(r.c[0]);
   const float D0 = static_cast<float>(dot_digits(ah[0], al[0]));
   const float D1 = static_cast<float>(dot_digits(ah[1], al[1]));
-  if constexpr (FMT == RTXLLM_FMT_IQ2S) {
+  if constexpr (fmt_is_iq2s(FMT)) {
     // d * (0.5 + n) / 4 * s = d * (n * s / 4 + s / 8)
     const float f0 = __builtin_fmaf(static_cast<float>(r.c[2] & 15u), ls.a0, ls.b0);
     const float f1 = __builtin_fmaf(static_cast<float>(r.c[2] >> 4), ls.a1, ls.b1);
@@ -606,7 +631,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     u = uvalid[i] ? u : units - 1u;
     ub[i] = u >> 3;
     uk[i] = u & 7u;
-    off[i] = unit_offsets<FMT>(ub[i], uk[i]);
+    off[i] = unit_offsets<FMT>(ub[i], uk[i], rows * bpr);
   }
 
   // Row strides and stream sizes in bytes (the host keeps every stream under
@@ -640,7 +665,8 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       std::uint32_t row = t * TILE + rr;
       row = row < rows ? row : rows - 1u;
 #pragma unroll
-      for (int i = 0; i < UPL; ++i) unit_load<FMT>(rsp, rsm, row * prow, row * mrow, off[i], raw[rr][i]);
+      for (int i = 0; i < UPL; ++i)
+        unit_load<FMT>(rsp, rsm, FMT == RTXLLM_FMT_IQ2S_UNITS ? row * bpr : row * prow, row * mrow, off[i], raw[rr][i]);
     }
   };
 

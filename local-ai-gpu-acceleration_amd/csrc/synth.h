@@ -91,7 +91,11 @@ RTXLLM_SYNTH_INLINE uint16_t rtxllm_synth_f16_uniform(uint64_t stream, uint64_t 
 
 /* Quant formats of the resident packs. Raw GGUF blocks except the Q4_K split
  * layouts, whose 128-byte nibble payload and per-block metadata live in two
- * separate streams. */
+ * separate streams, and IQ2S_UNITS: the same bytes as IQ2_S, regrouped over a
+ * tensor of N blocks (row-major) so that each 32-value unit k of block b reads
+ * three aligned fields: [0, 64 N) 8 B per unit (qs[4k..4k+3], signs[4k..4k+3])
+ * at 64 b + 8 k; [64 N, 80 N) 2 B per unit (qh[k], scales[k]) at 16 b + 2 k;
+ * [80 N, 82 N) the block's fp16 d at 2 b. */
 enum rtxllm_format {
   RTXLLM_FMT_Q4K_RAW = 0,             /* 144 B GGUF block */
   RTXLLM_FMT_Q4K_SPLIT_PREDECODED = 1, /* 128 B payload + 8 x (f32 S, f32 M) */
@@ -102,7 +106,8 @@ enum rtxllm_format {
   RTXLLM_FMT_IQ2S = 6,                 /* 82 B GGUF block */
   RTXLLM_FMT_IQ3S = 7,                 /* 110 B GGUF block */
   RTXLLM_FMT_Q4K_RAW_PREDECODED = 8,   /* 144 B GGUF block (quants) + 8 x (f32 S, f32 M) */
-  RTXLLM_FMT_COUNT = 9
+  RTXLLM_FMT_IQ2S_UNITS = 9,           /* IQ2_S blocks regrouped per 32-value unit (see below) */
+  RTXLLM_FMT_COUNT = 10
 };
 
 RTXLLM_SYNTH_INLINE uint32_t rtxllm_format_payload_bytes(int fmt) {
@@ -114,7 +119,8 @@ RTXLLM_SYNTH_INLINE uint32_t rtxllm_format_payload_bytes(int fmt) {
     case RTXLLM_FMT_Q4K_SPLIT_COMPACT:
     case RTXLLM_FMT_Q4K_SPLIT_NATIVE: return 128u;
     case RTXLLM_FMT_Q5K: return 176u;
-    case RTXLLM_FMT_IQ2S: return 82u;
+    case RTXLLM_FMT_IQ2S:
+    case RTXLLM_FMT_IQ2S_UNITS: return 82u;
     case RTXLLM_FMT_IQ3S: return 110u;
     default: return 0u;
   }

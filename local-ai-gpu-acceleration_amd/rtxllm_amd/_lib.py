@@ -52,6 +52,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_memory": [_P, _P, _P, _P],
     "rtxllm_stream_read": [_P, c_size_t, _P, _U, _S],
+    "rtxllm_iq2s_units_pack": [_P, _U, _U, _P, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",
@@ -80,6 +81,7 @@ _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_x16_bytes": (c_size_t, [c_uint32]),
     "rtxllm_matvec_batch_workspace": (c_size_t, [c_int, c_uint32, c_uint32]),
     "rtxllm_llama_destroy": (None, [_P]),
+    "rtxllm_llama_weights_changed": (None, [_P]),
     "rtxllm_llama_region": (_P, [_P, ctypes.c_char_p, _U, _P]),
     "rtxllm_llama_launches_per_step": (c_uint32, [_P]),
     "rtxllm_llama_graph_span_for": (c_uint32, [_P, _U]),

@@ -16,6 +16,7 @@ Q5K = 5
 IQ2S = 6
 IQ3S = 7
 Q4K_RAW_PREDECODED = 8
+IQ2S_UNITS = 9  # IQ2_S bytes regrouped per 32-value unit (packs.iq2s_units)
 
 BLOCK_VALUES = 256
 
@@ -29,6 +30,7 @@ PAYLOAD_BYTES = {
     IQ2S: 82,
     IQ3S: 110,
     Q4K_RAW_PREDECODED: 144,
+    IQ2S_UNITS: 82,
 }
 META_BYTES = {
     Q4K_SPLIT_PREDECODED: 64,
@@ -50,6 +52,7 @@ NAMES = {
     IQ2S: "iq2s",
     IQ3S: "iq3s",
     Q4K_RAW_PREDECODED: "q4k-raw-predecoded",
+    IQ2S_UNITS: "iq2s-units",
 }
 SPLIT_FORMATS = (Q4K_SPLIT_PREDECODED, Q4K_SPLIT_HALF, Q4K_SPLIT_COMPACT, Q4K_SPLIT_NATIVE)
 

@@ -57,6 +57,36 @@ def predecoded_pairs(raw: np.ndarray) -> np.ndarray:
     return q4k_split(F.Q4K_SPLIT_PREDECODED, raw)[1]
 
 
+def iq2s_unit_order(n_blocks: int) -> np.ndarray:
+    """Index array P with units[P] = raw for n_blocks GGUF IQ2_S blocks (82 B:
+    d, qs[32], signs[32], qh[8], scales[8]) in the IQ2S_UNITS layout: per unit
+    k of block b, qs[4k..4k+3] and signs[4k..4k+3] at 64 b + 8 k, (qh[k],
+    scales[k]) at 64 N + 16 b + 2 k, d at 80 N + 2 b."""
+    n = int(n_blocks)
+    b = np.arange(n, dtype=np.int64)[:, None]
+    i = np.arange(82, dtype=np.int64)[None, :]
+    k_qs, j_qs = (i - 2) // 4, (i - 2) % 4
+    k_sg, j_sg = (i - 34) // 4, (i - 34) % 4
+    pos = np.where(i < 2, 80 * n + 2 * b + i,
+          np.where(i < 34, 64 * b + 8 * k_qs + j_qs,
+          np.where(i < 66, 64 * b + 8 * k_sg + 4 + j_sg,
+          np.where(i < 74, 64 * n + 16 * b + 2 * (i - 66), 64 * n + 16 * b + 2 * (i - 74) + 1))))
+    return pos.reshape(-1)
+
+
+def iq2s_units(raw: np.ndarray) -> np.ndarray:
+    """GGUF IQ2_S blocks -> the IQ2S_UNITS layout (rtxllm_iq2s_units_pack on the host)."""
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    out = np.empty_like(raw)
+    out[iq2s_unit_order(raw.size // 82)] = raw
+    return out
+
+
+def iq2s_from_units(units: np.ndarray) -> np.ndarray:
+    units = np.ascontiguousarray(units, np.uint8).reshape(-1)
+    return units[iq2s_unit_order(units.size // 82)]
+
+
 def make_pack(fmt: int, rows: int, cols: int, seed: int, threads: int = 0) -> Pack:
     if fmt in F.SPLIT_FORMATS:
         raw = synth_raw(F.Q4K_RAW, rows, cols, seed, threads=threads)
@@ -65,6 +95,8 @@ def make_pack(fmt: int, rows: int, cols: int, seed: int, threads: int = 0) -> Pa
     if fmt == F.Q4K_RAW_PREDECODED:
         raw = synth_raw(F.Q4K_RAW, rows, cols, seed, threads=threads)
         return Pack(fmt, rows, cols, raw, predecoded_pairs(raw))
+    if fmt == F.IQ2S_UNITS:
+        return Pack(fmt, rows, cols, iq2s_units(synth_raw(F.IQ2S, rows, cols, seed, threads=threads)), None)
     return Pack(fmt, rows, cols, synth_raw(fmt, rows, cols, seed, threads=threads), None)
 
 

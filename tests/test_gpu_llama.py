@@ -193,6 +193,38 @@ def test_span_graph_rejects_bad_spans():
     m.close()
 
 
+def test_gate_up_unit_copy_follows_weight_changes():
+    """Batch 1 with IQ2_S gate/up: the matvec's unit-layout copy equals the
+    host regrouping of "gate_up" after the first step, and after an upload of
+    new gate/up weights a graph replay rebuilds it first, giving the eager
+    step's result on the new weights."""
+    s, pos, token = SMALL, 40, 3
+    m = build(s, pos)
+    sp = torch.cuda.Stream().cuda_stream
+    k0 = [m.download("k_cache", np.uint16, layer=l) for l in range(s.n_layers)]
+    m.graph_capture(sp)  # rebuilds the copies before capturing
+    torch.cuda.synchronize()
+    for l in range(s.n_layers):
+        assert np.array_equal(m.download("gate_up_units", np.uint8, layer=l),
+                              packs.iq2s_units(m.download("gate_up", np.uint8, layer=l)))
+    new = packs.synth_raw(F.IQ2S, 2 * s.ffn, s.hidden, seed=SEED + 777)
+    m.upload("gate_up", new, layer=1)
+
+    def run(step):
+        for l in range(s.n_layers):
+            m.upload("k_cache", k0[l], layer=l)
+        m.set_token_pos(token, pos)
+        step()
+        torch.cuda.synchronize()
+        return m.download("logits", np.float32)
+
+    replayed = run(lambda: m.graph_replay(sp))
+    assert np.array_equal(m.download("gate_up_units", np.uint8, layer=1), packs.iq2s_units(new))
+    eager = run(lambda: m.step(sp))
+    assert np.array_equal(replayed.view(np.uint32), eager.view(np.uint32))
+    m.close()
+
+
 def test_create_rejects_bad_configs():
     from rtxllm_amd._lib import HipError
 
