@@ -80,30 +80,37 @@ __device__ __forceinline__ void xg_zero(XG& g) {
 
 // Stage 16 values. Non-finite inputs stage as zero digits (their scale is kept,
 // so an infinite maximum still poisons the products, as fp32 would).
+// The digits come from Y = X + 128 as int16 (|X| <= 32512): H is Y's high byte
+// (floor((X + 128) / 256)) and L = X - 256 H its low byte minus 128 (the low
+// byte xor 0x80), so two int16 packs and two byte permutes give four values'
+// digit words; the group sum is 256 sum H + sum L, from two dot products.
 __device__ __forceinline__ void quant16(const float v[16], XG& g) {
+  typedef short short2_t __attribute__((ext_vector_type(2)));
   float m = 0.0f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[j]));
   const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
   g.s = m / kXQLimitF;
-  int total = 0;
+  int hsum = 0, lsum = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    std::uint32_t hw = 0u, lw = 0u;
+    int X[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      int X = static_cast<int>(rintf(v[4 * w + b] * inv));
-      X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
-      int H, L;
-      xq_digits(X, H, L);
-      hw |= (static_cast<std::uint32_t>(H) & 0xFFu) << (8 * b);
-      lw |= (static_cast<std::uint32_t>(L) & 0xFFu) << (8 * b);
-      total += X;
+      const int x = static_cast<int>(rintf(v[4 * w + b] * inv));
+      X[b] = x > kXQLimit ? kXQLimit : (x < -kXQLimit ? -kXQLimit : x);
     }
-    g.h[w] = hw;
-    g.l[w] = lw;
+    const short2_t bias = {128, 128};
+    const short2_t y01 = __builtin_amdgcn_cvt_pk_i16(X[0], X[1]) + bias;
+    const short2_t y23 = __builtin_amdgcn_cvt_pk_i16(X[2], X[3]) + bias;
+    const std::uint32_t u01 = __builtin_bit_cast(std::uint32_t, y01), u23 = __builtin_bit_cast(std::uint32_t, y23);
+    // byte i of the result: selector byte i, 0-3 = bytes of the second source, 4-7 of the first
+    g.h[w] = __builtin_amdgcn_perm(u23, u01, 0x07050301u);
+    g.l[w] = __builtin_amdgcn_perm(u23, u01, 0x06040200u) ^ 0x80808080u;
+    hsum = __builtin_amdgcn_sdot4(static_cast<int>(g.h[w]), 0x01010101, hsum, false);
+    lsum = __builtin_amdgcn_sdot4(static_cast<int>(g.l[w]), 0x01010101, lsum, false);
   }
-  g.sum = g.s * static_cast<float>(total);
+  g.sum = g.s * static_cast<float>(256 * hsum + lsum);
 }
 
 __device__ __forceinline__ void xg_load(const XQ& x, std::uint32_t group, XG& g) {
