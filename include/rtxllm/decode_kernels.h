@@ -258,6 +258,14 @@ hipError_t rtxllm_stream_read(const void* data, size_t bytes, uint32_t* out, uin
  * is 16-byte aligned and rows * cols / 256 * 82 bytes. */
 hipError_t rtxllm_iq2s_units_pack(const uint8_t* raw, uint32_t rows, uint32_t cols, uint8_t* out,
                                   hipStream_t stream);
+/* The same for GGUF IQ3_S blocks (format 7) -> IQ3S_UNITS (format 10, 114 B per
+ * block): per unit k of block b, qs[8k..8k+7] and signs[4k..4k+3] at 96 b +
+ * 12 k, (qh[k], scales[k / 2]) at 96 N + 16 b + 2 k, d at 112 N + 2 b. A unit
+ * then reads three aligned fields instead of five, for 4 more bytes per block
+ * (each scale byte is stored for both units that share it). The runner keeps
+ * unit copies of IQ3_S qkv and o weights at batch 1. */
+hipError_t rtxllm_iq3s_units_pack(const uint8_t* raw, uint32_t rows, uint32_t cols, uint8_t* out,
+                                  hipStream_t stream);
 
 /* Host-side helpers (no device work). */
 uint32_t rtxllm_format_payload_block_bytes(int format);

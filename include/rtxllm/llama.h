@@ -74,12 +74,13 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * [s * max_ctx / page_size, (s + 1) * max_ctx / page_size)).
  * Row layouts: qkv = q rows (n_heads*128) | k rows | v rows; gate_up rows
  * interleaved (2i = gate_i, 2i+1 = up_i).
- * Batch 1 with IQ2_S gate/up also holds "gate_up_units" per layer: the gate/up
- * weights regrouped into the IQ2S_UNITS layout (rtxllm_iq2s_units_pack), which
- * its matvec reads. The runner rebuilds a layer's copy before its next launch
- * after rtxllm_llama_upload of that layer's "gate_up", rtxllm_llama_load_packs
- * or rtxllm_llama_synth_weights; after writing "gate_up" through a region
- * pointer, call rtxllm_llama_weights_changed. */
+ * At batch 1 every IQ2_S / IQ3_S layer tensor (qkv, o, gate_up, down) also has
+ * "<role>_units" per layer: its weights regrouped into the IQ2S_UNITS /
+ * IQ3S_UNITS layout (rtxllm_iq2s_units_pack, rtxllm_iq3s_units_pack), which its
+ * matvec reads. The runner rebuilds a layer's copy before its next launch after
+ * rtxllm_llama_upload of that layer's tensor, rtxllm_llama_load_packs or
+ * rtxllm_llama_synth_weights; after writing a tensor through a region pointer,
+ * call rtxllm_llama_weights_changed. */
 void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes);
 /* The weights were written through region pointers: rebuild the derived unit
  * copies before the next launch (no counterpart in the reference). */

@@ -14,6 +14,8 @@ bool needs_meta(int fmt) { return rtxllm_format_meta_bytes(fmt) != 0u; }
 
 bool aligned(const void* p, std::uintptr_t a) { return (reinterpret_cast<std::uintptr_t>(p) % a) == 0u; }
 
+bool shape_ok(std::uint32_t rows, std::uint32_t cols) { return rows != 0u && cols != 0u && (cols % 256u) == 0u; }
+
 // The kernels issue 16-byte loads of x, of 16-byte aligned block fields and of
 // the Q4_K metadata records; reject pointers that break those alignments.
 bool pointers_ok(int fmt, const void* payload, const void* meta, const void* x) {
@@ -43,26 +45,49 @@ __global__ __launch_bounds__(256) void dequant_kernel(const std::uint8_t* __rest
   out[row * cols + b * 256u + threadIdx.x] = dequant_value<FMT>(p, m, threadIdx.x);
 }
 
-// IQ2S_UNITS: the workgroup gathers its block's 82 bytes back into the GGUF
-// order in LDS, then dequantises them exactly as IQ2_S.
-__global__ __launch_bounds__(256) void dequant_iq2s_units_kernel(const std::uint8_t* __restrict__ payload,
-                                                                 std::uint32_t cols, std::size_t nb,
-                                                                 float* __restrict__ out) {
-  __shared__ std::uint8_t blk[84];
+// Unit layouts: the workgroup gathers its block's bytes back into the GGUF
+// order in LDS, then dequantises them exactly as the GGUF format.
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_units_kernel(const std::uint8_t* __restrict__ payload,
+                                                            std::uint32_t cols, std::size_t nb,
+                                                            float* __restrict__ out) {
+  constexpr bool k2 = FMT == RTXLLM_FMT_IQ2S_UNITS;
+  constexpr std::uint32_t kRaw = k2 ? 82u : 110u;
+  __shared__ std::uint8_t blk[112];
   const std::size_t b = blockIdx.x;
   const std::uint32_t bpr = cols >> 8, i = threadIdx.x;
-  if (i < 82u) blk[i] = payload[iq2s_units_offset(b, i, nb)];
+  if (i < kRaw) blk[i] = payload[k2 ? iq2s_units_offset(b, i, nb) : iq3s_units_offset(b, i, nb)];
   __syncthreads();
-  out[(b / bpr) * cols + (b % bpr) * 256u + i] = dequant_value<RTXLLM_FMT_IQ2S>(blk, nullptr, i);
+  out[(b / bpr) * cols + (b % bpr) * 256u + i] =
+      dequant_value<k2 ? RTXLLM_FMT_IQ2S : RTXLLM_FMT_IQ3S>(blk, nullptr, i);
 }
 
-// One thread per block: GGUF IQ2_S bytes -> the unit layout.
-__global__ __launch_bounds__(256) void iq2s_units_pack_kernel(const std::uint8_t* __restrict__ raw, std::size_t nb,
-                                                              std::uint8_t* __restrict__ out) {
+// One thread per block: GGUF IQ2_S / IQ3_S bytes -> the unit layout (IQ3_S:
+// each scale byte also goes to the odd unit of its pair).
+template <int FMT>
+__global__ __launch_bounds__(256) void units_pack_kernel(const std::uint8_t* __restrict__ raw, std::size_t nb,
+                                                         std::uint8_t* __restrict__ out) {
+  constexpr bool k2 = FMT == RTXLLM_FMT_IQ2S_UNITS;
+  constexpr std::uint32_t kRaw = k2 ? 82u : 110u;
   const std::size_t b = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= nb) return;
-  const std::uint8_t* src = raw + 82u * b;
-  for (std::uint32_t i = 0; i < 82u; ++i) out[iq2s_units_offset(b, i, nb)] = src[i];
+  const std::uint8_t* src = raw + kRaw * b;
+  for (std::uint32_t i = 0; i < kRaw; ++i) {
+    const std::size_t o = k2 ? iq2s_units_offset(b, i, nb) : iq3s_units_offset(b, i, nb);
+    out[o] = src[i];
+    if (!k2 && i >= 106u) out[o + 2u] = src[i];  // (qh, scale) pair of unit 2j + 1
+  }
+}
+
+template <int FMT>
+hipError_t launch_units_pack(const std::uint8_t* raw, std::uint32_t rows, std::uint32_t cols, std::uint8_t* out,
+                             hipStream_t stream) {
+  if (!shape_ok(rows, cols) || raw == nullptr || out == nullptr || !aligned(out, 16)) return hipErrorInvalidValue;
+  const std::size_t nb = static_cast<std::size_t>(rows) * (cols / 256u);
+  if (nb * rtxllm_format_payload_bytes(FMT) > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(units_pack_kernel<FMT>, dim3(static_cast<unsigned>((nb + 255u) / 256u)), dim3(256), 0, stream,
+                     raw, nb, out);
+  return hipGetLastError();
 }
 
 template <int FMT>
@@ -73,8 +98,6 @@ hipError_t launch_dequant_fmt(const std::uint8_t* payload, const std::uint8_t* m
                      meta, cols, out);
   return hipGetLastError();
 }
-
-bool shape_ok(std::uint32_t rows, std::uint32_t cols) { return rows != 0u && cols != 0u && (cols % 256u) == 0u; }
 
 // Matvec + KV side-write + decode-chain token update (the reference's
 // *_decode launchers, decode_kernels.cu:4032-4072, 4473-4607).
@@ -115,10 +138,15 @@ extern "C" hipError_t rtxllm_dequant_f32(int format, const std::uint8_t* payload
     case RTXLLM_FMT_Q5K: return launch_dequant_fmt<RTXLLM_FMT_Q5K>(payload, meta, rows, cols, out, stream);
     case RTXLLM_FMT_IQ2S: return launch_dequant_fmt<RTXLLM_FMT_IQ2S>(payload, meta, rows, cols, out, stream);
     case RTXLLM_FMT_IQ3S: return launch_dequant_fmt<RTXLLM_FMT_IQ3S>(payload, meta, rows, cols, out, stream);
-    case RTXLLM_FMT_IQ2S_UNITS: {
+    case RTXLLM_FMT_IQ2S_UNITS:
+    case RTXLLM_FMT_IQ3S_UNITS: {
       const std::size_t nb = static_cast<std::size_t>(rows) * (cols / 256u);
-      hipLaunchKernelGGL(dequant_iq2s_units_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, payload,
-                         cols, nb, out);
+      if (format == RTXLLM_FMT_IQ2S_UNITS)
+        hipLaunchKernelGGL(dequant_units_kernel<RTXLLM_FMT_IQ2S_UNITS>, dim3(static_cast<unsigned>(nb)), dim3(256), 0,
+                           stream, payload, cols, nb, out);
+      else
+        hipLaunchKernelGGL(dequant_units_kernel<RTXLLM_FMT_IQ3S_UNITS>, dim3(static_cast<unsigned>(nb)), dim3(256), 0,
+                           stream, payload, cols, nb, out);
       return hipGetLastError();
     }
     case RTXLLM_FMT_Q4K_RAW_PREDECODED:
@@ -129,12 +157,12 @@ extern "C" hipError_t rtxllm_dequant_f32(int format, const std::uint8_t* payload
 
 extern "C" hipError_t rtxllm_iq2s_units_pack(const std::uint8_t* raw, std::uint32_t rows, std::uint32_t cols,
                                              std::uint8_t* out, hipStream_t stream) {
-  if (!shape_ok(rows, cols) || raw == nullptr || out == nullptr || !aligned(out, 16)) return hipErrorInvalidValue;
-  const std::size_t nb = static_cast<std::size_t>(rows) * (cols / 256u);
-  if (nb * 82u > 0xFFFFFFFFull) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(iq2s_units_pack_kernel, dim3(static_cast<unsigned>((nb + 255u) / 256u)), dim3(256), 0, stream, raw,
-                     nb, out);
-  return hipGetLastError();
+  return launch_units_pack<RTXLLM_FMT_IQ2S_UNITS>(raw, rows, cols, out, stream);
+}
+
+extern "C" hipError_t rtxllm_iq3s_units_pack(const std::uint8_t* raw, std::uint32_t rows, std::uint32_t cols,
+                                             std::uint8_t* out, hipStream_t stream) {
+  return launch_units_pack<RTXLLM_FMT_IQ3S_UNITS>(raw, rows, cols, out, stream);
 }
 
 extern "C" hipError_t rtxllm_matvec(int format, const std::uint8_t* payload, const std::uint8_t* meta,

@@ -46,11 +46,16 @@ struct rtxllm_llama {
   // (output phase: LM head + argmax)
   rtxllm::LayerExecutionPlan layer_plan, head_plan;
   rtxllm::AdmissionDecision admission;
-  // Batch 1 with IQ2_S gate/up: the matvec reads a copy in the IQ2S_UNITS
-  // layout ("gate_up_units"), rebuilt from "gate_up" before the next launch
+  // Batch 1: the matvecs of IQ2_S / IQ3_S tensors read copies in the unit
+  // layouts ("<role>_units"), rebuilt from "<role>" before the next launch
   // after the layer's weights change (upload, synthesis, packs).
-  bool units = false;
-  std::vector<char> units_dirty;
+  struct UnitCopy {
+    std::string role;
+    int fmt;  // the unit layout
+    std::uint32_t rows, cols;
+  };
+  std::vector<UnitCopy> unit_copies;
+  std::vector<char> units_dirty;  // [copy * n_layers + layer]
 };
 
 namespace {
@@ -110,19 +115,42 @@ void mark_units_dirty(rtxllm_llama* m) {
   std::fill(m->units_dirty.begin(), m->units_dirty.end(), 1);
 }
 
-// Rebuild the unit copies of the layers whose gate/up weights changed (stream
-// ordered after the writes; a device-to-device regrouping, no allocation).
+// The unit layout of a GGUF IQ format (-1: none).
+int units_of(int fmt) {
+  return fmt == RTXLLM_FMT_IQ2S ? RTXLLM_FMT_IQ2S_UNITS : fmt == RTXLLM_FMT_IQ3S ? RTXLLM_FMT_IQ3S_UNITS : -1;
+}
+
+// The copy of `role` (-1: the role's matvec reads the GGUF layout).
+int unit_copy(const rtxllm_llama* m, const char* role) {
+  for (std::size_t i = 0; i < m->unit_copies.size(); ++i)
+    if (m->unit_copies[i].role == role) return static_cast<int>(i);
+  return -1;
+}
+
+// Rebuild the unit copies of the layers whose weights changed (stream ordered
+// after the writes; a device-to-device regrouping, no allocation).
 hipError_t ensure_units(rtxllm_llama* m, hipStream_t stream) {
-  if (!m->units) return hipSuccess;
-  for (std::uint32_t l = 0; l < m->cfg.n_layers; ++l) {
-    if (!m->units_dirty[l]) continue;
-    const hipError_t st = rtxllm_iq2s_units_pack(
-        static_cast<const std::uint8_t*>(m->arena.arena_ptr(layer_name("gate_up", l))), 2u * m->cfg.ffn,
-        m->cfg.hidden, static_cast<std::uint8_t*>(m->arena.arena_ptr(layer_name("gate_up_units", l))), stream);
-    if (st != hipSuccess) return st;
-    m->units_dirty[l] = 0;
+  const std::uint32_t L = m->cfg.n_layers;
+  for (std::size_t i = 0; i < m->unit_copies.size(); ++i) {
+    const rtxllm_llama::UnitCopy& u = m->unit_copies[i];
+    for (std::uint32_t l = 0; l < L; ++l) {
+      if (!m->units_dirty[i * L + l]) continue;
+      const auto* raw = static_cast<const std::uint8_t*>(m->arena.arena_ptr(layer_name(u.role.c_str(), l)));
+      auto* out = static_cast<std::uint8_t*>(m->arena.arena_ptr(layer_name((u.role + "_units").c_str(), l)));
+      const hipError_t st = u.fmt == RTXLLM_FMT_IQ2S_UNITS ? rtxllm_iq2s_units_pack(raw, u.rows, u.cols, out, stream)
+                                                           : rtxllm_iq3s_units_pack(raw, u.rows, u.cols, out, stream);
+      if (st != hipSuccess) return st;
+      m->units_dirty[i * L + l] = 0;
+    }
   }
   return hipSuccess;
+}
+
+// The tensor a batch-1 matvec of `role` (format fmt) reads, and its format.
+TensorRef tensor_for(const rtxllm_llama* m, const char* role, std::uint32_t l, int fmt, int& read_fmt) {
+  const int u = unit_copy(m, role);
+  read_fmt = u >= 0 ? m->unit_copies[static_cast<std::size_t>(u)].fmt : fmt;
+  return tensor(m, layer_name(u >= 0 ? (std::string(role) + "_units").c_str() : role, l));
 }
 
 hipError_t synth_tensor(rtxllm_llama* m, const std::string& name, int fmt, std::uint32_t rows, std::uint32_t cols,
@@ -174,8 +202,15 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   m->partial_floats = rtxllm::attention_partials_floats(c.n_heads, c.n_kv_heads, c.max_ctx);
   m->batch = batch;
   m->span = c.max_ctx;
-  m->units = batch == 1u && c.fmt_gate_up == RTXLLM_FMT_IQ2S;
-  m->units_dirty.assign(m->units ? c.n_layers : 0u, 1);
+  if (batch == 1u) {
+    const rtxllm_llama::UnitCopy roles[] = {{"qkv", c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden},
+                                            {"o", c.fmt_o, c.hidden, m->q_rows},
+                                            {"gate_up", c.fmt_gate_up, 2u * c.ffn, c.hidden},
+                                            {"down", c.fmt_down, c.hidden, c.ffn}};
+    for (const auto& r : roles)
+      if (units_of(r.fmt) >= 0) m->unit_copies.push_back({r.role, units_of(r.fmt), r.rows, r.cols});
+  }
+  m->units_dirty.assign(m->unit_copies.size() * c.n_layers, 1);
   m->pages_per_seq = c.max_ctx / c.page_size;
   const std::size_t B = batch;
 
@@ -186,8 +221,8 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     add_tensor(specs, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden);
     add_tensor(specs, layer_name("o", l), c.fmt_o, c.hidden, m->q_rows);
     add_tensor(specs, layer_name("gate_up", l), c.fmt_gate_up, 2u * c.ffn, c.hidden);
-    if (batch == 1u && c.fmt_gate_up == RTXLLM_FMT_IQ2S)
-      add_tensor(specs, layer_name("gate_up_units", l), RTXLLM_FMT_IQ2S_UNITS, 2u * c.ffn, c.hidden);
+    for (const auto& u : m->unit_copies)
+      add_tensor(specs, layer_name((u.role + "_units").c_str(), l), u.fmt, u.rows, u.cols);
     add_tensor(specs, layer_name("down", l), c.fmt_down, c.hidden, c.ffn);
     specs.push_back({layer_name("attn_norm", l), 4u * c.hidden});
     specs.push_back({layer_name("ffn_norm", l), 4u * c.hidden});
@@ -318,8 +353,10 @@ extern "C" void rtxllm_llama_destroy(rtxllm_llama* m) { delete m; }
 
 extern "C" void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, size_t* bytes) {
   if (m == nullptr || name == nullptr) return nullptr;
-  static const char* kPerLayer[] = {"qkv", "qkv_meta", "o", "o_meta", "gate_up", "gate_up_meta", "gate_up_units", "down",
-                                    "down_meta", "attn_norm", "ffn_norm", "k_cache", "v_cache", "block_table"};
+  static const char* kPerLayer[] = {"qkv",       "qkv_meta",  "qkv_units", "o",           "o_meta",
+                                    "o_units",   "gate_up",   "gate_up_meta", "gate_up_units", "down",
+                                    "down_meta", "down_units", "attn_norm", "ffn_norm",  "k_cache",
+                                    "v_cache",   "block_table"};
   std::string key = name;
   for (const char* p : kPerLayer)
     if (key == p) {
@@ -338,7 +375,8 @@ extern "C" hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uin
   std::size_t size = 0;
   auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
   if (base == nullptr || src == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
-  if (m->units && std::strcmp(name, "gate_up") == 0) m->units_dirty[layer] = 1;
+  const int u = unit_copy(m, name);
+  if (u >= 0) m->units_dirty[static_cast<std::size_t>(u) * m->cfg.n_layers + layer] = 1;
   return hipMemcpy(base + offset, src, bytes, hipMemcpyHostToDevice);
 }
 
@@ -634,8 +672,9 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
       return rtxllm::launch_embed_q5k(embed ? region<std::uint8_t>(m, "embed") : nullptr, c.hidden, c.vocab,
                                       region<std::uint32_t>(m, "token"), h, next_norm, xq, sumsq, m->nslots, stream);
     case kQkv: {
-      const TensorRef t = tensor(m, layer_name("qkv", l));
-      return rtxllm::launch_qkv(c.fmt_qkv, t.payload, t.meta, c.hidden, in, m->q_rows, m->kv_rows,
+      int f = 0;
+      const TensorRef t = tensor_for(m, "qkv", l, c.fmt_qkv, f);
+      return rtxllm::launch_qkv(f, t.payload, t.meta, c.hidden, in, m->q_rows, m->kv_rows,
                                 region<float2>(m, "rope"), c.max_ctx, pos, m->arena.arena_ptr("q"), kv_layer(m, l),
                                 stream);
     }
@@ -644,19 +683,21 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
                                       region<float>(m, "attn_partials"), region<float>(m, "att"),
                                       m->arena.arena_ptr("xq_att"), stream);
     case kO: {
-      const TensorRef t = tensor(m, layer_name("o", l));
-      return rtxllm::launch_residual(c.fmt_o, t.payload, t.meta, c.hidden, m->q_rows, m->arena.arena_ptr("xq_att"),
+      int f = 0;
+      const TensorRef t = tensor_for(m, "o", l, c.fmt_o, f);
+      return rtxllm::launch_residual(f, t.payload, t.meta, c.hidden, m->q_rows, m->arena.arena_ptr("xq_att"),
                                      nullptr, h,
                                      region<float>(m, layer_name("ffn_norm", l)), xq, sumsq, stream);
     }
     case kGateUp: {
-      const TensorRef t = tensor(m, layer_name(m->units ? "gate_up_units" : "gate_up", l));
-      return rtxllm::launch_gate_up(m->units ? RTXLLM_FMT_IQ2S_UNITS : c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn,
-                                    c.hidden, in, region<float>(m, "act"), stream);
+      int f = 0;
+      const TensorRef t = tensor_for(m, "gate_up", l, c.fmt_gate_up, f);
+      return rtxllm::launch_gate_up(f, t.payload, t.meta, 2u * c.ffn, c.hidden, in, region<float>(m, "act"), stream);
     }
     case kDown: {
-      const TensorRef t = tensor(m, layer_name("down", l));
-      return rtxllm::launch_residual(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, nullptr, region<float>(m, "act"), h,
+      int f = 0;
+      const TensorRef t = tensor_for(m, "down", l, c.fmt_down, f);
+      return rtxllm::launch_residual(f, t.payload, t.meta, c.hidden, c.ffn, nullptr, region<float>(m, "act"), h,
                                      next_norm, xq, sumsq, stream);
     }
     case kHead: {

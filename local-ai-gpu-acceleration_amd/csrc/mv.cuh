@@ -29,6 +29,7 @@ namespace rtxllm {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x3 __attribute__((ext_vector_type(3)));
 
 struct QTensor {
   const std::uint8_t* payload;  // raw blocks, or the Q4_K split payload stream
@@ -55,9 +56,13 @@ struct XSrc {
 // same cache lines, which only the L1 turns into one L2 request per line, so
 // those loads keep the default policy.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr bool fmt_is_iq(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S || f == RTXLLM_FMT_IQ2S_UNITS; }
-// IQ2_S values in either layout (same codebooks, same arithmetic).
+constexpr bool fmt_is_iq(int f) {
+  return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ3S || f == RTXLLM_FMT_IQ2S_UNITS || f == RTXLLM_FMT_IQ3S_UNITS;
+}
+// IQ2_S values in either layout (same codebooks, same arithmetic); the rest
+// of the IQ formats are IQ3_S.
 constexpr bool fmt_is_iq2s(int f) { return f == RTXLLM_FMT_IQ2S || f == RTXLLM_FMT_IQ2S_UNITS; }
+constexpr bool fmt_is_units(int f) { return f == RTXLLM_FMT_IQ2S_UNITS || f == RTXLLM_FMT_IQ3S_UNITS; }
 template <int FMT>
 constexpr int load_policy() {
   return (fmt_is_iq(FMT) || FMT == RTXLLM_FMT_Q5K) ? 0 : 2;  // 2 = nt
@@ -207,6 +212,7 @@ struct FmtBytes {
   static constexpr std::uint32_t payload = FMT == RTXLLM_FMT_Q5K ? 176u
                                            : fmt_is_iq2s(FMT) ? 82u
                                            : FMT == RTXLLM_FMT_IQ3S ? 110u
+                                           : FMT == RTXLLM_FMT_IQ3S_UNITS ? 114u
                                            : fmt_is_raw_q4k(FMT) ? 144u : 128u;
   static constexpr std::uint32_t meta = FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED ? 64u
                                         : FMT == RTXLLM_FMT_Q4K_SPLIT_HALF ? 32u
@@ -224,8 +230,18 @@ __host__ __device__ inline std::size_t iq2s_units_offset(std::size_t b, std::uin
   return 64u * nb + 16u * b + 2u * (i - 74u) + 1u;                      // scales
 }
 
-// nb: blocks in the tensor (the unit layout's field streams start at 64 nb and
-// 80 nb); the IQ2S_UNITS offsets are relative to the row's first block.
+// Byte i (GGUF order: d, qs[64], qh[8], signs[32], scales[4]) of block b of an
+// IQ3S_UNITS tensor of nb blocks (a scale byte: its copy in the even unit).
+__host__ __device__ inline std::size_t iq3s_units_offset(std::size_t b, std::uint32_t i, std::size_t nb) {
+  if (i < 2u) return 112u * nb + 2u * b + i;                              // d
+  if (i < 66u) return 96u * b + 12u * ((i - 2u) >> 3) + ((i - 2u) & 7u);  // qs
+  if (i < 74u) return 96u * nb + 16u * b + 2u * (i - 66u);                // qh
+  if (i < 106u) return 96u * b + 12u * ((i - 74u) >> 2) + 8u + ((i - 74u) & 3u);  // signs
+  return 96u * nb + 16u * b + 4u * (i - 106u) + 1u;                       // scales (unit 2j)
+}
+
+// nb: blocks in the tensor (where the unit layouts' field streams start); the
+// unit-layout offsets are relative to the row's first block.
 template <int FMT>
 __device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k, std::uint32_t nb) {
   UnitOff u{};
@@ -235,6 +251,10 @@ __device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k
     u.o[0] = 64u * b + 8u * k;             // qs, signs of the unit
     u.o[1] = 64u * nb + 16u * b + 2u * k;  // qh, scales of the unit
     u.o[2] = 80u * nb + 2u * b;            // d
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S_UNITS) {
+    u.o[0] = 96u * b + 12u * k;            // qs (8 B), signs (4 B) of the unit
+    u.o[1] = 96u * nb + 16u * b + 2u * k;  // qh, scale byte of the unit
+    u.o[2] = 112u * nb + 2u * b;           // d
   } else if constexpr (fmt_is_iq2s(FMT)) {
     u.o[0] = pb;                 // d
     u.o[1] = pb + 2u + 4u * k;   // qs (grid low bytes)
@@ -288,7 +308,7 @@ __device__ __forceinline__ void unit_groups(std::uint32_t b, std::uint32_t k, st
 }
 
 // rp / rm: this row's start in the payload / metadata stream (wave-uniform);
-// IQ2S_UNITS: sp = blocks before this row.
+// unit layouts: sp = blocks before this row.
 template <int FMT>
 __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, std::uint32_t sm, const UnitOff& u,
                                           UnitRaw& r) {
@@ -303,6 +323,12 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
     const u32x2 q = bld_u64<P>(rp, u.o[0], 64u * sp);
     r.a[0] = q.x, r.a[1] = q.y;
+    const std::uint32_t hs = bld_u16<P>(rp, u.o[1], 16u * sp);
+    r.c[1] = hs & 0xFFu, r.c[2] = hs >> 8;
+    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
+  } else if constexpr (FMT == RTXLLM_FMT_IQ3S_UNITS) {
+    const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rp, u.o[0], 96u * sp, P);
+    r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z;
     const std::uint32_t hs = bld_u16<P>(rp, u.o[1], 16u * sp);
     r.c[1] = hs & 0xFFu, r.c[2] = hs >> 8;
     r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
@@ -666,7 +692,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       row = row < rows ? row : rows - 1u;
 #pragma unroll
       for (int i = 0; i < UPL; ++i)
-        unit_load<FMT>(rsp, rsm, FMT == RTXLLM_FMT_IQ2S_UNITS ? row * bpr : row * prow, row * mrow, off[i], raw[rr][i]);
+        unit_load<FMT>(rsp, rsm, fmt_is_units(FMT) ? row * bpr : row * prow, row * mrow, off[i], raw[rr][i]);
     }
   };
 

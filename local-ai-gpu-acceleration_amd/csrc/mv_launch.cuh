@@ -134,6 +134,7 @@ inline bool mv_geometry(int fmt, std::uint32_t rows, std::uint32_t cols, MvGeom&
     case RTXLLM_FMT_Q5K: return mv_geometry_fmt<RTXLLM_FMT_Q5K, SELF, Epi>(rows, cols, g);
     case RTXLLM_FMT_IQ2S: return mv_geometry_fmt<RTXLLM_FMT_IQ2S, SELF, Epi>(rows, cols, g);
     case RTXLLM_FMT_IQ2S_UNITS: return mv_geometry_fmt<RTXLLM_FMT_IQ2S_UNITS, SELF, Epi>(rows, cols, g);
+    case RTXLLM_FMT_IQ3S_UNITS: return mv_geometry_fmt<RTXLLM_FMT_IQ3S_UNITS, SELF, Epi>(rows, cols, g);
     case RTXLLM_FMT_IQ3S: return mv_geometry_fmt<RTXLLM_FMT_IQ3S, SELF, Epi>(rows, cols, g);
     case RTXLLM_FMT_Q4K_RAW_PREDECODED:
       return mv_geometry_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED, SELF, Epi>(rows, cols, g);
@@ -157,6 +158,7 @@ inline hipError_t launch_mv(int fmt, const QTensor& w, const XSrc& xs, std::uint
     case RTXLLM_FMT_Q5K: return launch_mv_fmt<RTXLLM_FMT_Q5K, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_IQ2S: return launch_mv_fmt<RTXLLM_FMT_IQ2S, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_IQ2S_UNITS: return launch_mv_fmt<RTXLLM_FMT_IQ2S_UNITS, SELF>(w, xs, row_count, epi, stream);
+    case RTXLLM_FMT_IQ3S_UNITS: return launch_mv_fmt<RTXLLM_FMT_IQ3S_UNITS, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_IQ3S: return launch_mv_fmt<RTXLLM_FMT_IQ3S, SELF>(w, xs, row_count, epi, stream);
     case RTXLLM_FMT_Q4K_RAW_PREDECODED:
       return launch_mv_fmt<RTXLLM_FMT_Q4K_RAW_PREDECODED, SELF>(w, xs, row_count, epi, stream);

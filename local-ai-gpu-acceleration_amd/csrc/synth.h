@@ -95,7 +95,10 @@ RTXLLM_SYNTH_INLINE uint16_t rtxllm_synth_f16_uniform(uint64_t stream, uint64_t 
  * tensor of N blocks (row-major) so that each 32-value unit k of block b reads
  * three aligned fields: [0, 64 N) 8 B per unit (qs[4k..4k+3], signs[4k..4k+3])
  * at 64 b + 8 k; [64 N, 80 N) 2 B per unit (qh[k], scales[k]) at 16 b + 2 k;
- * [80 N, 82 N) the block's fp16 d at 2 b. */
+ * [80 N, 82 N) the block's fp16 d at 2 b. IQ3S_UNITS likewise for IQ3_S (d, qs[64],
+ * qh[8], signs[32], scales[4]): [0, 96 N) 12 B per unit (qs[8k..8k+7],
+ * signs[4k..4k+3]) at 96 b + 12 k; [96 N, 112 N) (qh[k], scales[k / 2]) at
+ * 16 b + 2 k (each scale byte twice); [112 N, 114 N) d at 2 b. */
 enum rtxllm_format {
   RTXLLM_FMT_Q4K_RAW = 0,             /* 144 B GGUF block */
   RTXLLM_FMT_Q4K_SPLIT_PREDECODED = 1, /* 128 B payload + 8 x (f32 S, f32 M) */
@@ -107,7 +110,8 @@ enum rtxllm_format {
   RTXLLM_FMT_IQ3S = 7,                 /* 110 B GGUF block */
   RTXLLM_FMT_Q4K_RAW_PREDECODED = 8,   /* 144 B GGUF block (quants) + 8 x (f32 S, f32 M) */
   RTXLLM_FMT_IQ2S_UNITS = 9,           /* IQ2_S blocks regrouped per 32-value unit (see below) */
-  RTXLLM_FMT_COUNT = 10
+  RTXLLM_FMT_IQ3S_UNITS = 10,          /* IQ3_S blocks regrouped per 32-value unit, 114 B per block */
+  RTXLLM_FMT_COUNT = 11
 };
 
 RTXLLM_SYNTH_INLINE uint32_t rtxllm_format_payload_bytes(int fmt) {
@@ -122,6 +126,7 @@ RTXLLM_SYNTH_INLINE uint32_t rtxllm_format_payload_bytes(int fmt) {
     case RTXLLM_FMT_IQ2S:
     case RTXLLM_FMT_IQ2S_UNITS: return 82u;
     case RTXLLM_FMT_IQ3S: return 110u;
+    case RTXLLM_FMT_IQ3S_UNITS: return 114u;
     default: return 0u;
   }
 }

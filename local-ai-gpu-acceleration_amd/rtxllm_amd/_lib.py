@@ -53,6 +53,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_memory": [_P, _P, _P, _P],
     "rtxllm_stream_read": [_P, c_size_t, _P, _U, _S],
     "rtxllm_iq2s_units_pack": [_P, _U, _U, _P, _S],
+    "rtxllm_iq3s_units_pack": [_P, _U, _U, _P, _S],
 }
 for _name in (
     "rtxllm_launch_q4k_matvec_decode",

@@ -17,6 +17,7 @@ IQ2S = 6
 IQ3S = 7
 Q4K_RAW_PREDECODED = 8
 IQ2S_UNITS = 9  # IQ2_S bytes regrouped per 32-value unit (packs.iq2s_units)
+IQ3S_UNITS = 10  # IQ3_S bytes regrouped per 32-value unit (packs.iq3s_units), 114 B per block
 
 BLOCK_VALUES = 256
 
@@ -31,6 +32,7 @@ PAYLOAD_BYTES = {
     IQ3S: 110,
     Q4K_RAW_PREDECODED: 144,
     IQ2S_UNITS: 82,
+    IQ3S_UNITS: 114,
 }
 META_BYTES = {
     Q4K_SPLIT_PREDECODED: 64,
@@ -41,6 +43,7 @@ META_BYTES = {
 }
 # GGUF bytes per block of the source format: the roofline's algorithmic bytes.
 GGUF_BLOCK_BYTES = {f: (144 if f in (0, 1, 2, 3, 4, 8) else PAYLOAD_BYTES[f]) for f in PAYLOAD_BYTES}
+GGUF_BLOCK_BYTES[IQ3S_UNITS] = 110
 
 NAMES = {
     Q4K_RAW: "q4k-raw",
@@ -53,6 +56,7 @@ NAMES = {
     IQ3S: "iq3s",
     Q4K_RAW_PREDECODED: "q4k-raw-predecoded",
     IQ2S_UNITS: "iq2s-units",
+    IQ3S_UNITS: "iq3s-units",
 }
 SPLIT_FORMATS = (Q4K_SPLIT_PREDECODED, Q4K_SPLIT_HALF, Q4K_SPLIT_COMPACT, Q4K_SPLIT_NATIVE)
 

@@ -87,6 +87,40 @@ def iq2s_from_units(units: np.ndarray) -> np.ndarray:
     return units[iq2s_unit_order(units.size // 82)]
 
 
+def iq3s_unit_order(n_blocks: int) -> np.ndarray:
+    """Index array P with units[P] = raw for n_blocks GGUF IQ3_S blocks (110 B:
+    d, qs[64], qh[8], signs[32], scales[4]) in the IQ3S_UNITS layout (114 B per
+    block): per unit k of block b, qs[8k..8k+7] and signs[4k..4k+3] at
+    96 b + 12 k, (qh[k], scales[k / 2]) at 96 N + 16 b + 2 k, d at 112 N + 2 b;
+    a scale byte's place here is its copy in the even unit of its pair."""
+    n = int(n_blocks)
+    b = np.arange(n, dtype=np.int64)[:, None]
+    i = np.arange(110, dtype=np.int64)[None, :]
+    pos = np.where(i < 2, 112 * n + 2 * b + i,
+          np.where(i < 66, 96 * b + 12 * ((i - 2) // 8) + (i - 2) % 8,
+          np.where(i < 74, 96 * n + 16 * b + 2 * (i - 66),
+          np.where(i < 106, 96 * b + 12 * ((i - 74) // 4) + 8 + (i - 74) % 4,
+                   96 * n + 16 * b + 4 * (i - 106) + 1))))
+    return pos.reshape(-1)
+
+
+def iq3s_units(raw: np.ndarray) -> np.ndarray:
+    """GGUF IQ3_S blocks -> the IQ3S_UNITS layout (rtxllm_iq3s_units_pack on the host)."""
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    n = raw.size // 110
+    out = np.empty(114 * n, np.uint8)
+    order = iq3s_unit_order(n)
+    out[order] = raw
+    scales = order.reshape(n, 110)[:, 106:].reshape(-1)  # even-unit copies; the odd unit's is 2 bytes on
+    out[scales + 2] = raw.reshape(n, 110)[:, 106:].reshape(-1)
+    return out
+
+
+def iq3s_from_units(units: np.ndarray) -> np.ndarray:
+    units = np.ascontiguousarray(units, np.uint8).reshape(-1)
+    return units[iq3s_unit_order(units.size // 114)]
+
+
 def make_pack(fmt: int, rows: int, cols: int, seed: int, threads: int = 0) -> Pack:
     if fmt in F.SPLIT_FORMATS:
         raw = synth_raw(F.Q4K_RAW, rows, cols, seed, threads=threads)
@@ -97,6 +131,8 @@ def make_pack(fmt: int, rows: int, cols: int, seed: int, threads: int = 0) -> Pa
         return Pack(fmt, rows, cols, raw, predecoded_pairs(raw))
     if fmt == F.IQ2S_UNITS:
         return Pack(fmt, rows, cols, iq2s_units(synth_raw(F.IQ2S, rows, cols, seed, threads=threads)), None)
+    if fmt == F.IQ3S_UNITS:
+        return Pack(fmt, rows, cols, iq3s_units(synth_raw(F.IQ3S, rows, cols, seed, threads=threads)), None)
     return Pack(fmt, rows, cols, synth_raw(fmt, rows, cols, seed, threads=threads), None)
 
 

@@ -193,11 +193,11 @@ def test_span_graph_rejects_bad_spans():
     m.close()
 
 
-def test_gate_up_unit_copy_follows_weight_changes():
-    """Batch 1 with IQ2_S gate/up: the matvec's unit-layout copy equals the
-    host regrouping of "gate_up" after the first step, and after an upload of
-    new gate/up weights a graph replay rebuilds it first, giving the eager
-    step's result on the new weights."""
+def test_unit_copies_follow_weight_changes():
+    """Batch 1 with IQ3_S q/k/v/o and IQ2_S gate/up: the matvecs' unit-layout
+    copies equal the host regrouping of their tensors after capture, and after
+    an upload of new gate/up weights a graph replay rebuilds that copy first,
+    giving the eager step's result on the new weights."""
     s, pos, token = SMALL, 40, 3
     m = build(s, pos)
     sp = torch.cuda.Stream().cuda_stream
@@ -207,6 +207,9 @@ def test_gate_up_unit_copy_follows_weight_changes():
     for l in range(s.n_layers):
         assert np.array_equal(m.download("gate_up_units", np.uint8, layer=l),
                               packs.iq2s_units(m.download("gate_up", np.uint8, layer=l)))
+        for role in ("qkv", "o"):
+            assert np.array_equal(m.download(role + "_units", np.uint8, layer=l),
+                                  packs.iq3s_units(m.download(role, np.uint8, layer=l)))
     new = packs.synth_raw(F.IQ2S, 2 * s.ffn, s.hidden, seed=SEED + 777)
     m.upload("gate_up", new, layer=1)
 

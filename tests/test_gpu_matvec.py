@@ -31,13 +31,15 @@ def oracle_fmt(fmt: int) -> int:
 
 
 def oracle_args(pack: packs.Pack):
-    """The oracle has no raw+predecoded or IQ2_S unit layout; feed it the
+    """The oracle has no raw+predecoded or unit layout; feed it the
     split-predecoded equivalent (same quants, same pairs) or the GGUF blocks."""
     if pack.fmt == F.Q4K_RAW_PREDECODED:
         pl = pack.payload.reshape(-1, 144)[:, 16:].copy().reshape(-1)
         return F.Q4K_SPLIT_PREDECODED, pl, pack.meta
     if pack.fmt == F.IQ2S_UNITS:  # the same bytes in GGUF block order
         return F.IQ2S, packs.iq2s_from_units(pack.payload), None
+    if pack.fmt == F.IQ3S_UNITS:
+        return F.IQ3S, packs.iq3s_from_units(pack.payload), None
     return pack.fmt, pack.payload, pack.meta
 
 
@@ -236,21 +238,28 @@ def test_matvec_xq_equals_self_staging_and_staged_oracle(orc, fmt, shape):
     assert np.max(np.abs(y_xq - ref64)) / np.max(np.abs(ref64)) < 1e-4
 
 
+UNIT_CASES = [(F.IQ2S, F.IQ2S_UNITS, "rtxllm_iq2s_units_pack", packs.iq2s_units),
+              (F.IQ3S, F.IQ3S_UNITS, "rtxllm_iq3s_units_pack", packs.iq3s_units)]
+
+
+@pytest.mark.parametrize("case", UNIT_CASES, ids=["iq2s", "iq3s"])
 @pytest.mark.parametrize("shape", [(1, 256), (133, 4096), (48, 14336)])
-def test_iq2s_units_pack_and_matvec_bit_identical(shape):
-    """rtxllm_iq2s_units_pack writes the host restatement's bytes, and the unit
+def test_units_pack_and_matvec_bit_identical(case, shape):
+    """The unit-layout packers write the host restatement's bytes, and the unit
     layout's matvecs (fp32 x and staged x) equal the GGUF layout's bit for bit."""
+    fmt, ufmt, packer, host = case
     rows, cols = shape
-    raw = packs.synth_raw(F.IQ2S, rows, cols, seed=7100 + rows)
+    raw = packs.synth_raw(fmt, rows, cols, seed=7100 + rows + fmt)
     d_raw = ops.to_dev(raw)
-    d_units = torch.empty_like(d_raw)
-    assert lib().rtxllm_iq2s_units_pack(ops.ptr(d_raw), rows, cols, ops.ptr(d_units), ops.stream()) == 0
+    d_units = torch.empty(F.PAYLOAD_BYTES[ufmt] * rows * (cols // 256), dtype=torch.uint8, device="cuda:0")
+    assert getattr(lib(), packer)(ops.ptr(d_raw), rows, cols, ops.ptr(d_units), ops.stream()) == 0
     torch.cuda.synchronize()
-    assert np.array_equal(d_units.cpu().numpy(), packs.iq2s_units(raw))
+    assert np.array_equal(d_units.cpu().numpy(), host(raw))
     x = ops.to_dev(packs.normal_f32(7200 + cols, cols))
-    y_raw = ops.matvec(ops.DevicePack(packs.Pack(F.IQ2S, rows, cols, raw, None)), x).cpu().numpy()
-    units = ops.DevicePack(packs.Pack(F.IQ2S_UNITS, rows, cols, packs.iq2s_units(raw), None))
+    gguf = ops.DevicePack(packs.Pack(fmt, rows, cols, raw, None))
+    units = ops.DevicePack(packs.Pack(ufmt, rows, cols, host(raw), None))
+    y_raw = ops.matvec(gguf, x).cpu().numpy()
     assert np.array_equal(ops.matvec(units, x).cpu().numpy().view(np.uint32), y_raw.view(np.uint32))
     xq = ops.stage(x)
-    y_raw_xq = ops.matvec_xq(ops.DevicePack(packs.Pack(F.IQ2S, rows, cols, raw, None)), xq).cpu().numpy()
+    y_raw_xq = ops.matvec_xq(gguf, xq).cpu().numpy()
     assert np.array_equal(ops.matvec_xq(units, xq).cpu().numpy().view(np.uint32), y_raw_xq.view(np.uint32))

@@ -1,7 +1,8 @@
-"""CPU checks of the IQ2S_UNITS layout's host restatement (packs.iq2s_units),
-which the GPU packer must match byte for byte: the regrouping is a bijection
-of the tensor's bytes, it inverts, and hand-placed fields of a two-block
-tensor land where the layout puts them."""
+"""CPU checks of the unit layouts' host restatements (packs.iq2s_units,
+packs.iq3s_units), which the GPU packers must match byte for byte: the
+regrouping is a bijection of the tensor's bytes (IQ3_S: plus one copy of each
+scale byte), it inverts, and hand-placed fields of a two-block tensor land
+where the layout puts them."""
 
 from __future__ import annotations
 
@@ -38,3 +39,23 @@ def test_unit_format_sizes():
     assert F.meta_bytes(F.IQ2S_UNITS) == 0
     pack = packs.make_pack(F.IQ2S_UNITS, 3, 512, seed=5)
     assert np.array_equal(packs.iq2s_from_units(pack.payload), packs.make_pack(F.IQ2S, 3, 512, seed=5).payload)
+
+
+def test_iq3s_unit_order_and_fields_by_hand():
+    for n in (1, 3, 40):
+        order = packs.iq3s_unit_order(n)
+        assert len(set(order.tolist())) == 110 * n and order.max() < 114 * n
+        raw = np.random.default_rng(n).integers(0, 256, 110 * n, dtype=np.uint8)
+        u = packs.iq3s_units(raw)
+        assert np.array_equal(packs.iq3s_from_units(u), raw)
+        # every unit's (qh, scale) pair: the scale byte of its pair of units
+        pairs = u[96 * n: 112 * n].reshape(n, 8, 2)
+        assert np.array_equal(pairs[:, :, 0], raw.reshape(n, 110)[:, 66:74])
+        assert np.array_equal(pairs[:, :, 1], np.repeat(raw.reshape(n, 110)[:, 106:110], 2, axis=1))
+    n = 2
+    raw = np.array([(100 * b + i) % 256 for b in range(n) for i in range(110)], np.uint8)
+    u = packs.iq3s_units(raw)
+    # unit 5 of block 1: qs bytes 2 + 40 .. 2 + 47, sign bytes 74 + 20 .. 74 + 23
+    assert list(u[96 + 60: 96 + 72]) == [(100 + i) % 256 for i in list(range(42, 50)) + list(range(94, 98))]
+    assert list(u[112 * n: 114 * n]) == [0, 1, 100, 101]
+    assert F.PAYLOAD_BYTES[F.IQ3S_UNITS] == 114 and F.GGUF_BLOCK_BYTES[F.IQ3S_UNITS] == 110
