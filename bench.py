@@ -264,7 +264,7 @@ def context_buckets(torch, m, stream, token, batch: int, steps: int) -> dict:
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = REPO / "profiles" / "decode_8b_hbm_traffic.txt"
 STAGE_KERNELS = {  # decode stage -> substring of its kernel's name
-    "qkv": "EpiQkv", "attention": "attn_partial_kernel", "o": "mv_kernel<7, 1, 4, false, rtxllm::(anonymous "
+    "qkv": "EpiQkv", "attention": "attn_partial_kernel", "o": "mv_kernel<10, 1, 4, false, rtxllm::(anonymous "
     "namespace)::EpiResidual", "gate_up": "EpiGateUp", "down": "mv_kernel<4, 1, 4, true", "lm_head": "EpiLogits",
 }
 
