@@ -54,6 +54,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time a plain streaming read (rtxllm_stream_read) of each stage's byte count over "
                          "rotating HBM-cold buffers and print it as JSON, nothing else")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="run the batch-8 matvec stages of one layer (the matrix-core counter workload)")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
+                    help="matrix-core FLOP and rate per batch matvec kernel from the counter and trace runs")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -287,6 +291,61 @@ def traffic_probe(torch) -> None:
     m.close()
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 matrix-core peak
+MFMA_STAGES = ("qkv", "o", "gate_up", "down", "lm_head")
+
+
+def mfma_probe(torch) -> None:
+    """The workload of the matrix-core counter pass: the batch-8 decode step's
+    matvec stages of layer 0 (8 sequences at ~4030 positions), three times each."""
+    import dataclasses
+
+    from rtxllm_amd.llama import LLAMA_8B
+
+    shape = dataclasses.replace(LLAMA_8B, batch=8)
+    m, token = build_model(torch, shape)
+    m.set_token_pos(token, [shape.max_ctx - 64] * 8)
+    sp = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        for st in MFMA_STAGES:
+            m.launch_stage(0, st, sp)
+    torch.cuda.synchronize()
+    m.close()
+
+
+def mfma_summary(pmc_dir: str, trace_dir: str) -> str:
+    """Per batch matvec kernel: fp16 matrix-core FLOP per dispatch from
+    SQ_INSTS_VALU_MFMA_MOPS_F16 (units of 512 FLOP), the algorithmic FLOP of the
+    8-sequence product (2 rows cols 16: 8 sequences x hi/lo columns), the mean
+    dispatch time from the kernel trace of the same workload, and the achieved
+    rate against the dense fp16 peak."""
+    import csv
+    import glob
+
+    mops: dict = {}
+    for f in glob.glob(str(Path(pmc_dir) / "**" / "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == "SQ_INSTS_VALU_MFMA_MOPS_F16" and "mm_kernel" in r["Kernel_Name"]:
+                mops.setdefault((r["Kernel_Name"], r["Grid_Size"]), []).append(float(r["Counter_Value"]))
+    dur: dict = {}
+    for f in glob.glob(str(Path(trace_dir) / "**" / "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if "mm_kernel" in r["Kernel_Name"]:
+                g = str(int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+                us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                dur.setdefault((r["Kernel_Name"], g), []).append(us)
+    lines = []
+    for (name, grid), v in sorted(mops.items(), key=lambda kv: kv[0]):
+        flop = 512.0 * sum(v) / len(v)
+        d = dur.get((name, grid))
+        us = sum(d) / len(d) if d else float("nan")
+        short = name.replace("rtxllm::(anonymous namespace)::", "").replace("rtxllm::", "").replace("void ", "")
+        short = short.split("(")[0]
+        lines.append(f"{short} grid {grid}: mfma_flop {flop:.4g} us {us:.2f} TFLOP/s {flop / us / 1e6:.2f} "
+                     f"frac_of_fp16_peak {flop / us / 1e6 / MFMA_PEAK_TFLOPS:.5f}")
+    return "\n".join(lines) + "\n"
+
+
 def traffic_summary(fetch_dir: str, write_dir: str) -> str:
     """Per-kernel mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
     true bytes / counter bytes of a calibration kernel: the sum (reads
@@ -518,11 +577,17 @@ def main() -> int:
     if args.traffic_summary:
         sys.stdout.write(traffic_summary(*args.traffic_summary))
         return 0
+    if args.mfma_summary:
+        sys.stdout.write(mfma_summary(*args.mfma_summary))
+        return 0
     import torch
 
     torch.cuda.set_device(0)
     if args.traffic_probe:
         traffic_probe(torch)
+        return 0
+    if args.mfma_probe:
+        mfma_probe(torch)
         return 0
     if args.read_ceiling:
         print(json.dumps({"read_ceiling": read_ceiling(torch)}), flush=True)
