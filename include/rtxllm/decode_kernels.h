@@ -240,6 +240,13 @@ size_t rtxllm_matvec_batch_workspace(int format, uint32_t rows, uint32_t cols);
 hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
                                float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same from the fp32 activation x [batch][cols] (16-byte aligned): every
+ * wave stages its own 512 columns with the rtxllm_stage_batch rule, so the
+ * result equals rtxllm_stage_batch + rtxllm_matvec_batch bit for bit without
+ * the staging launch (the batch decode step's down projection). */
+hipError_t rtxllm_matvec_batch_f32(int format, const uint8_t* payload, const uint8_t* meta, const float* x,
+                                   float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Measurement helper, no counterpart in the reference: a plain streaming read
  * of `bytes` (a multiple of 16, 16-byte aligned) by `workgroups` workgroups of

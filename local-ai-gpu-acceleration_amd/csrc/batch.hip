@@ -193,14 +193,14 @@ struct MmLogits {
 
 // Workgroups of mm_kernel<FMT, Epi> of `threads` threads resident per CU (0 if
 // the query fails), cached per size.
-template <int FMT, class Epi>
+template <int FMT, class Epi, bool SELF = false>
 int mm_resident(std::uint32_t threads) {
   static int cache[kMaxPanels + 1] = {};
   const std::uint32_t w = threads / 64u;
   if (w == 0u || w > kMaxPanels) return 0;
   if (cache[w] == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mm_kernel<FMT, Epi>),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mm_kernel<FMT, Epi, SELF>),
                                                      static_cast<int>(threads), 0) != hipSuccess || n <= 0)
       return 0;
     cache[w] = n;
@@ -229,11 +229,11 @@ inline bool mm_split(int fmt, std::uint32_t rows, std::uint32_t cols, MmGeom& g)
 
 // Persistent grid: the workgroups resident at once, shared by the panel groups,
 // every workgroup taking the same number of tiles (but the last few).
-template <int FMT, class Epi>
+template <int FMT, class Epi, bool SELF = false>
 bool mm_geom(std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
   if (!mm_split(FMT, rows, cols, g)) return false;
   const std::uint32_t tiles = (rows + 15u) / 16u;
-  const int resident = mm_resident<FMT, Epi>(64u * g.ppg);
+  const int resident = mm_resident<FMT, Epi, SELF>(64u * g.ppg);
   const std::uint32_t per_cu = resident > 0 ? static_cast<std::uint32_t>(resident) : 1u;
   const std::uint32_t cap = std::max(1u, per_cu * static_cast<std::uint32_t>(num_cus()) / g.groups);
   const std::uint32_t rounds = (tiles + cap - 1u) / cap;
@@ -241,31 +241,33 @@ bool mm_geom(std::uint32_t rows, std::uint32_t cols, MmGeom& g) {
   return true;
 }
 
-template <int FMT, class Epi>
+template <int FMT, bool SELF = false, class Epi>
 hipError_t launch_mm_epi(const QTensor& w, const void* x16, std::uint32_t batch, const Epi& epi, bool one_group,
                          MmGeom* geom, hipStream_t stream) {
   MmGeom g;
-  if (!mm_geom<FMT, Epi>(w.rows, w.cols, g) || batch == 0u || batch > kBatchMax || x16 == nullptr ||
+  if (!mm_geom<FMT, Epi, SELF>(w.rows, w.cols, g) || batch == 0u || batch > kBatchMax || x16 == nullptr ||
       (one_group && g.groups != 1u))
     return hipErrorInvalidValue;
   const std::uint64_t blocks = static_cast<std::uint64_t>(w.rows) * (w.cols / 256u);
   if (blocks * FmtBytes<FMT>::payload > 0xFFFFFFFFull || blocks * FmtBytes<FMT>::meta > 0xFFFFFFFFull)
     return hipErrorInvalidValue;
   if (geom != nullptr) *geom = g;
-  hipLaunchKernelGGL((mm_kernel<FMT, Epi>), dim3(g.grid, g.groups), dim3(64u * g.ppg), 0, stream, w, x16, batch, epi);
+  hipLaunchKernelGGL((mm_kernel<FMT, Epi, SELF>), dim3(g.grid, g.groups), dim3(64u * g.ppg), 0, stream, w, x16, batch,
+                     epi);
   return hipGetLastError();
 }
 
-template <class Epi>
+// SELF: x16 is the fp32 activation [batch][cols] (the kernel stages it).
+template <class Epi, bool SELF = false>
 hipError_t launch_mm(int fmt, const QTensor& w, const void* x16, std::uint32_t batch, const Epi& epi, bool one_group,
                      MmGeom* geom, hipStream_t stream) {
   switch (fmt) {
-    case RTXLLM_FMT_IQ2S: return launch_mm_epi<RTXLLM_FMT_IQ2S>(w, x16, batch, epi, one_group, geom, stream);
-    case RTXLLM_FMT_IQ3S: return launch_mm_epi<RTXLLM_FMT_IQ3S>(w, x16, batch, epi, one_group, geom, stream);
-    case RTXLLM_FMT_Q5K: return launch_mm_epi<RTXLLM_FMT_Q5K>(w, x16, batch, epi, one_group, geom, stream);
-    case RTXLLM_FMT_Q4K_RAW: return launch_mm_epi<RTXLLM_FMT_Q4K_RAW>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_IQ2S: return launch_mm_epi<RTXLLM_FMT_IQ2S, SELF>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_IQ3S: return launch_mm_epi<RTXLLM_FMT_IQ3S, SELF>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_Q5K: return launch_mm_epi<RTXLLM_FMT_Q5K, SELF>(w, x16, batch, epi, one_group, geom, stream);
+    case RTXLLM_FMT_Q4K_RAW: return launch_mm_epi<RTXLLM_FMT_Q4K_RAW, SELF>(w, x16, batch, epi, one_group, geom, stream);
     case RTXLLM_FMT_Q4K_SPLIT_NATIVE:
-      return launch_mm_epi<RTXLLM_FMT_Q4K_SPLIT_NATIVE>(w, x16, batch, epi, one_group, geom, stream);
+      return launch_mm_epi<RTXLLM_FMT_Q4K_SPLIT_NATIVE, SELF>(w, x16, batch, epi, one_group, geom, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -306,6 +308,16 @@ hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   return launch_mm(fmt, w, x16, batch, MmStore{out, rows, batch}, false, nullptr, stream);
+}
+
+hipError_t launch_mm_batch_self(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                                std::uint32_t cols, const float* x, std::uint32_t batch, float* out,
+                                hipStream_t stream) {
+  if (payload == nullptr || out == nullptr || (fmt == RTXLLM_FMT_Q4K_SPLIT_NATIVE && meta == nullptr) ||
+      (reinterpret_cast<std::uintptr_t>(x) % 16u) != 0u)
+    return hipErrorInvalidValue;
+  const QTensor w{payload, meta, rows, cols};
+  return launch_mm<MmStore, true>(fmt, w, x, batch, MmStore{out, rows, batch}, false, nullptr, stream);
 }
 
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,
@@ -387,9 +399,12 @@ extern "C" size_t rtxllm_matvec_batch_workspace(int format, uint32_t rows, uint3
   return mm_batch_workspace_bytes(format, rows, cols);
 }
 
-extern "C" hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
-                                          float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
-                                          size_t workspace_bytes, hipStream_t stream) {
+namespace {
+
+// x16 is the staged buffer, or with self_stage the fp32 activation [batch][cols].
+hipError_t matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x, bool self_stage,
+                        float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
   if (y == nullptr || batch == 0u || batch > kBatchMax) return hipErrorInvalidValue;
   const std::uint32_t groups = mm_panel_groups(format, rows, cols);
   if (groups == 0u) return hipErrorInvalidValue;
@@ -399,9 +414,26 @@ extern "C" hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, co
     if (workspace == nullptr || workspace_bytes < 4u * n * groups) return hipErrorInvalidValue;
     out = static_cast<float*>(workspace);
   }
-  hipError_t st = launch_mm_batch(format, payload, meta, rows, cols, x16, batch, out, stream);
+  hipError_t st = self_stage ? launch_mm_batch_self(format, payload, meta, rows, cols, static_cast<const float*>(x),
+                                                    batch, out, stream)
+                             : launch_mm_batch(format, payload, meta, rows, cols, x, batch, out, stream);
   if (st != hipSuccess || groups == 1u) return st;
   hipLaunchKernelGGL(mm_reduce_kernel, dim3(static_cast<unsigned>((n + 255u) / 256u)), dim3(256), 0, stream,
                      static_cast<const float*>(workspace), groups, static_cast<std::uint32_t>(n), y);
   return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
+                                          float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  return matvec_batch(format, payload, meta, x16, false, y, rows, cols, batch, workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t rtxllm_matvec_batch_f32(int format, const uint8_t* payload, const uint8_t* meta, const float* x,
+                                              float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
+                                              size_t workspace_bytes, hipStream_t stream) {
+  if (x == nullptr) return hipErrorInvalidValue;
+  return matvec_batch(format, payload, meta, x, true, y, rows, cols, batch, workspace, workspace_bytes, stream);
 }

@@ -123,6 +123,12 @@ std::size_t mm_batch_workspace_bytes(int fmt, std::uint32_t rows, std::uint32_t 
 // out[g][s][row] = panel group g's part of (W x_s)[row] (out = y with one group).
 hipError_t launch_mm_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
                            std::uint32_t cols, const void* x16, std::uint32_t batch, float* out, hipStream_t stream);
+// The same with the activation given as fp32 x [batch][cols] (16-byte aligned):
+// each wave stages its own panel (the plain x16 rule), so no staging launch is
+// needed between the producer of x and this matvec.
+hipError_t launch_mm_batch_self(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
+                                std::uint32_t cols, const float* x, std::uint32_t batch, float* out,
+                                hipStream_t stream);
 // qkv of every sequence with the batch-1 qkv epilogue's RoPE and KV append at
 // pos[s], the KV block table of sequence s being row s (table_stride entries).
 hipError_t launch_mm_qkv_batch(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t cols,

@@ -312,7 +312,10 @@ struct MmStore {
 // thread (a thread only ever sees one sequence), epi(row, s, y, y of row ^ 1),
 // and epi.finish(wave, lane, waves) after the last tile. Epilogues other than
 // MmStore need a single panel group.
-template <int FMT, class Epi>
+// SELF: x16 is instead the fp32 activation [batch][cols], staged by each wave
+// for its own panel with the plain staging rule (block exponent from the
+// block's max |x|, hi / lo fp16 halves), so no staging launch precedes it.
+template <int FMT, class Epi, bool SELF = false>
 __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const void* __restrict__ x16,
                                                              std::uint32_t batch, Epi epi) {
   // per-panel partial C of a tile, double buffered by tile parity
@@ -326,21 +329,59 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t tiles = (rows + 15u) >> 4;
 
   // B operands of the panel: its blocks x 8 instructions, 1 KB of whole lanes each.
-  constexpr int PB = kPanelBlocks;
-  const uint4* xb = reinterpret_cast<const uint4*>(x16) + PB * panel * 8u * 64u + lane;
-  uint4 B[PB][8];
-#pragma unroll
-  for (int b = 0; b < PB; ++b)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
-
   // The lane's C column is n = lane % 16 = 2 s + hi/lo: its products of block
   // b of the panel carry that sequence's block exponent, 2^e[s][b].
-  const X16Tail tail = x16_tail(x16, cols);
+  constexpr int PB = kPanelBlocks;
   const std::uint32_t nb = cols >> 8;
+  uint4 B[PB][8];
   float fb[PB];
+  if constexpr (SELF) {
+    // lane (q, n = 2 s + h) holds values 256 kb + 64 q + 8 j + i of sequence s
+    // in instruction j of block kb; the 4 lanes of a column (q = 0..3) cover
+    // the block, so its max is two exchanges away
+    const std::uint32_t n = lane & 15u, s = n >> 1;
+    const bool ok = s < batch;
+    const float* xr = static_cast<const float*>(x16) + static_cast<std::size_t>(ok ? s : 0u) * cols +
+                      256u * (PB * panel) + 64u * q;
 #pragma unroll
-  for (int b = 0; b < PB; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + PB * panel + b]);
+    for (int b = 0; b < PB; ++b) {
+      float v[64];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float4 t = reinterpret_cast<const float4*>(xr + 256u * b)[j];
+        v[4 * j] = ok ? t.x : 0.0f, v[4 * j + 1] = ok ? t.y : 0.0f;
+        v[4 * j + 2] = ok ? t.z : 0.0f, v[4 * j + 3] = ok ? t.w : 0.0f;
+      }
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) m = fmaxf(m, fabsf(v[i]));
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      int e = 0;
+      if (m > 0.0f && m <= 3.0e38f) frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+      fb[b] = ldexpf(1.0f, e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float t = ldexpf(v[8 * j + i], -e);
+          const _Float16 hi = static_cast<_Float16>(t);
+          h[i] = (n & 1u) ? static_cast<_Float16>(t - static_cast<float>(hi)) : hi;
+        }
+        B[b][j] = __builtin_bit_cast(uint4, h);
+      }
+    }
+  } else {
+    const uint4* xb = reinterpret_cast<const uint4*>(x16) + PB * panel * 8u * 64u + lane;
+#pragma unroll
+    for (int b = 0; b < PB; ++b)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
+    const X16Tail tail = x16_tail(x16, cols);
+#pragma unroll
+    for (int b = 0; b < PB; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + PB * panel + b]);
+  }
 
   // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
   // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
@@ -350,10 +391,13 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
   const bool t_store = (t_n & 1u) == 0u && t_s < batch;
   float t_post = 1.0f;
-  if (*tail.eps >= 0.0f) {
-    float ss = 0.0f;
-    for (std::uint32_t b = 0; b < nb; ++b) ss += tail.ss[t_s * nb + b];
-    t_post = 1.0f / sqrtf(ss / static_cast<float>(cols) + *tail.eps);
+  if constexpr (!SELF) {
+    const X16Tail tail = x16_tail(x16, cols);
+    if (*tail.eps >= 0.0f) {
+      float ss = 0.0f;
+      for (std::uint32_t b = 0; b < nb; ++b) ss += tail.ss[t_s * nb + b];
+      t_post = 1.0f / sqrtf(ss / static_cast<float>(cols) + *tail.eps);
+    }
   }
   epi.init(t_s);
 

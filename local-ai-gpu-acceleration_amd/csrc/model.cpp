@@ -289,7 +289,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     gd.name = "decode";
     gd.batch_bucket = batch;
     gd.phase_count = static_cast<std::uint32_t>(c.n_layers * m->layer_plan.phase_count + m->head_plan.phase_count);
-    gd.kernel_launches_per_replay = batch > 1u ? 1u + 9u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
+    gd.kernel_launches_per_replay = batch > 1u ? 1u + 8u * c.n_layers + 2u : 1u + 6u * c.n_layers + 2u;
     gd.workspace_high_water_bytes = req.workspace_bytes;
     req.graph_bytes = rtxllm::estimate_hip_graph_bucket_allocation(gd).total_bytes;
     m->graph_desc = gd;
@@ -630,14 +630,14 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
     }
     case kGateUp: {
       const TensorRef t = tensor(m, layer_name("gate_up", l));
-      hipError_t st = rtxllm::launch_mm_gate_up_batch(c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn, c.hidden, x16, B,
-                                                      region<float>(m, "act"), stream);
-      if (st != hipSuccess) return st;
-      return rtxllm::launch_stage_batch(region<float>(m, "act"), B, c.ffn, x16, stream);
+      // act [B][ffn] goes to the down projection in fp32: its waves stage it
+      return rtxllm::launch_mm_gate_up_batch(c.fmt_gate_up, t.payload, t.meta, 2u * c.ffn, c.hidden, x16, B,
+                                             region<float>(m, "act"), stream);
     }
     case kDown: {
       const TensorRef t = tensor(m, layer_name("down", l));
-      hipError_t st = rtxllm::launch_mm_batch(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn, x16, B, work, stream);
+      hipError_t st = rtxllm::launch_mm_batch_self(c.fmt_down, t.payload, t.meta, c.hidden, c.ffn,
+                                                   region<float>(m, "act"), B, work, stream);
       if (st != hipSuccess) return st;
       return rtxllm::launch_rms_stage_batch(h, work, m->groups_down, nullptr, nullptr, 0u, next_norm, c.rms_eps,
                                             c.hidden, B, x16, stream);
@@ -770,8 +770,10 @@ extern "C" hipError_t rtxllm_llama_step(rtxllm_llama* m, hipStream_t stream) {
 
 extern "C" uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m) {
   if (m == nullptr) return 0u;
-  // batch: qkv 1, attention 3 (partials, combine, staging), o / gate-up / down 2 each
-  return m->batch > 1u ? 1u + 9u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
+  // batch, per layer: qkv 1, attention 2 (partials; combine + staging of att),
+  // o 2 and down 2 (matvec; residual + RMSNorm staging), gate/up 1 (the down
+  // matvec stages act itself)
+  return m->batch > 1u ? 1u + 8u * m->cfg.n_layers + 2u : 1u + 6u * m->cfg.n_layers + 2u;
 }
 
 namespace {

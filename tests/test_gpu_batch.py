@@ -66,6 +66,30 @@ def test_batch_sequences_are_independent(orc):
         assert np.array_equal(y1[0], y8[s])
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 4096, 8), (300, 1024, 3), (64, 14336, 8), (48, 512, 1)])
+def test_batch_matvec_f32_equals_staged(fmt, rows, cols, batch):
+    """rtxllm_matvec_batch_f32 (each wave stages its own columns) gives
+    rtxllm_stage_batch + rtxllm_matvec_batch bit for bit, with activations
+    from 1e-3 to 1e3 so that the block exponents differ."""
+    from rtxllm_amd._lib import lib
+
+    pack = packs.make_pack(fmt, rows, cols, 9100 + fmt)
+    w = ops.DevicePack(pack)
+    scales = np.array([1e-3, 1.0, 1e3, 0.5, 7.0, 1e-2, 30.0, 2.0], np.float32)[:batch, None]
+    xs = (np.stack([packs.normal_f32(9200 + s, cols) for s in range(batch)]) * scales).astype(np.float32)
+    xd = ops.to_dev(xs)
+    y_staged = ops.matvec_batch(w, ops.stage_batch(xd), batch).cpu().numpy()
+    need = int(lib().rtxllm_matvec_batch_workspace(fmt, rows, cols))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda:0")
+    y = torch.empty((batch, rows), dtype=torch.float32, device="cuda:0")
+    rc = lib().rtxllm_matvec_batch_f32(fmt, ops.ptr(w.payload), ops.ptr(w.meta), ops.ptr(xd), ops.ptr(y), rows, cols,
+                                       batch, ops.ptr(ws) if need else None, need, ops.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), y_staged.view(np.uint32))
+
+
 def test_batch_invalid_arguments():
     pack = packs.make_pack(F.IQ2S, 16, 768, 1)
     w = ops.DevicePack(pack)

@@ -185,7 +185,7 @@ def test_batch_regions_and_launch_count(model):
     assert m.region_bytes("logits") == 4 * B * s.vocab
     assert m.region_bytes("block_table", 0) == 4 * B * pps
     assert m.region_bytes("k_cache", 0) == 2 * B * pps * s.n_kv_heads * s.page_size * HEAD_DIM
-    assert m.launches_per_step() == 1 + 9 * s.n_layers + 2
+    assert m.launches_per_step() == 1 + 8 * s.n_layers + 2
 
 
 def test_batch_create_rejects_bad_configs():
