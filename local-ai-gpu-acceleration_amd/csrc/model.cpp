@@ -66,9 +66,10 @@ std::size_t blocks_of(std::uint32_t rows, std::uint32_t cols) {
   return static_cast<std::size_t>(rows) * (cols / 256u);
 }
 
-// Configurable tensor formats (the unit layout is the runner's own copy).
+// Configurable tensor formats (the unit layouts are the runner's own copies).
 bool format_ok(int fmt) {
-  return fmt >= RTXLLM_FMT_Q4K_RAW && fmt < RTXLLM_FMT_COUNT && fmt != RTXLLM_FMT_IQ2S_UNITS;
+  return fmt >= RTXLLM_FMT_Q4K_RAW && fmt < RTXLLM_FMT_COUNT && fmt != RTXLLM_FMT_IQ2S_UNITS &&
+         fmt != RTXLLM_FMT_IQ3S_UNITS;
 }
 
 std::string layer_name(const char* role, std::uint32_t layer) {

@@ -236,3 +236,7 @@ def test_create_rejects_bad_configs():
         kw.update(bad)
         with pytest.raises(HipError):
             Llama(Shape(**kw))
+    # the unit layouts are the runner's own copies, not configurable formats
+    for fmt in (F.IQ2S_UNITS, F.IQ3S_UNITS):
+        with pytest.raises(HipError):
+            Llama(SMALL, formats=dict(fmt_gate_up=fmt))
