@@ -54,6 +54,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time a plain streaming read (rtxllm_stream_read) of each stage's byte count over "
                          "rotating HBM-cold buffers and print it as JSON, nothing else")
+    ap.add_argument("--units-sweep", action="store_true",
+                    help="time the IQ decode matvecs in the GGUF and the unit layouts (batch 1, HBM-cold)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run the batch-8 matvec stages of one layer (the matrix-core counter workload)")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
@@ -462,6 +464,28 @@ def q4k_sweep(torch) -> dict:
     return out
 
 
+UNIT_SWEEP = [("gate_up", 6, 9, 28672, 4096), ("iq2s_14336x4096", 6, 9, 14336, 4096),
+              ("qkv", 7, 10, 6144, 4096), ("o", 7, 10, 4096, 4096)]
+
+
+def units_sweep(torch) -> dict:
+    """Batch-1 matvec (staged x, HBM-cold) of each IQ decode shape in the GGUF
+    layout and in its unit layout (IQ2S_UNITS / IQ3S_UNITS): us and GB/s of the
+    GGUF bytes, and the unit layout's resident bytes."""
+    from rtxllm_amd import formats as F
+
+    stream = torch.cuda.Stream()
+    out = {}
+    for name, fmt, ufmt, rows, cols in UNIT_SWEEP:
+        ab = F.algorithmic_bytes(fmt, rows, cols)
+        us, _, _ = time_matvec(torch, stream, fmt, rows, cols, 0x5EED0001)
+        uus, _, ubytes = time_matvec(torch, stream, ufmt, rows, cols, 0x5EED0001)
+        out[name] = {"shape": f"{rows}x{cols}", "gguf_us": round(us, 3), "gguf_GBps": round(ab / us / 1e3, 1),
+                     "units_us": round(uus, 3), "units_GBps": round(ab / uus / 1e3, 1),
+                     "units_resident_bytes": int(ubytes), "gguf_bytes": int(ab), "speedup": round(us / uus, 3)}
+    return out
+
+
 READ_SIZES = {"o": 7208960, "qkv": 10813440, "attention": 16777216, "iq2s_14336x4096": 18882560,
               "down": 33030144, "gate_up": 37617664, "lm_head": 361168896}
 
@@ -594,6 +618,9 @@ def main() -> int:
         return 0
     if args.q4k_sweep:
         print(json.dumps({"q4k_sweep": q4k_sweep(torch)}), flush=True)
+        return 0
+    if args.units_sweep:
+        print(json.dumps({"units_sweep": units_sweep(torch)}), flush=True)
         return 0
     dec = decode_bench(torch, args)
     dom = dec["stages"][dec["dominant"]]
