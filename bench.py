@@ -193,6 +193,26 @@ def decode_bench(torch, args, batch: int = 1) -> dict:
     pos_end = m.download("pos", np.uint32)
     assert all(int(p) == pos0 + total for p in pos_end), (pos_end, pos0, total)
     tokens = [int(t) for t in m.download("token", np.uint32)]
+    assert m.status(sp) == [0] * batch  # no sequence reached the end of its context
+
+    # latency distribution (the reference reports p50 / p95 / p99 of its replays,
+    # main.cpp:4838-4913): the same replays from the same positions, one event
+    # after each, so each step's device time is the gap between two events
+    m.set_token_pos(token, [pos0] * batch if batch > 1 else pos0)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            m.graph_replay(sp)
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        evs[0].record(stream)
+        for i in range(args.steps):
+            m.graph_replay(sp)
+            evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])
+    latency = {f"p{q}": round(float(np.percentile(per_step, q)), 5) for q in (50, 95, 99)}
+    latency.update({"mean": round(float(per_step.mean()), 5), "max": round(float(per_step.max()), 5),
+                    "unit": "ms per step", "steps": args.steps})
 
     wb = layer_weight_bytes(shape)
     mean_ctx = pos0 + args.warmup + (args.steps + 1) / 2.0
@@ -223,7 +243,7 @@ def decode_bench(torch, args, batch: int = 1) -> dict:
     buckets = None if args.no_context_buckets else context_buckets(torch, m, stream, token, batch, args.steps)
     m.close()
     return {
-        "ms_per_step": ms, "tok_s": batch * 1e3 / ms, "wall_s": wall, "step_bytes": step_bytes,
+        "ms_per_step": ms, "tok_s": batch * 1e3 / ms, "wall_s": wall, "step_bytes": step_bytes, "latency": latency,
         "GB/s": step_bytes / (ms * 1e-3) / 1e9, "stages": stages, "dominant": dom, "launches": launches,
         "mean_context": mean_ctx, "tokens_after": tokens, "context_buckets": buckets,
     }
@@ -496,7 +516,7 @@ def read_ceiling(torch) -> dict:
     the best of four grid sizes), one launch per buffer over rotating buffers
     spanning more than twice the MALL (HBM-cold), in a hipGraph like the
     stages."""
-    from rtxllm_amd._lib import check, lib
+    from rtxllm_amd._lib import check, probe_lib
 
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
@@ -509,7 +529,7 @@ def read_ceiling(torch) -> dict:
         for grid in (1024, 2048, 4096, 8192):
             def run(grid=grid):
                 for b in bufs:
-                    check("rtxllm_stream_read", lib().rtxllm_stream_read(b.data_ptr(), nbytes, res.data_ptr(), grid,
+                    check("rtxllm_stream_read", probe_lib().rtxllm_stream_read(b.data_ptr(), nbytes, res.data_ptr(), grid,
                                                                           sp))
 
             us = time_graph(torch, stream, run, reps=5) * 1e3 / k
@@ -524,10 +544,37 @@ def read_ceiling(torch) -> dict:
 
 # ---- CPU baseline -------------------------------------------------------------
 
+def cpu_info() -> dict:
+    """Host CPU model, sockets, cores and threads (lscpu when present), and the
+    CPUs this process may run on."""
+    import subprocess
+
+    info = {"model": _cpu_model(), "online_cpus": os.cpu_count()}
+    try:
+        info["usable_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)", "CPU max MHz",
+                     "L3 cache"):
+                info["lscpu " + k] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
 def cpu_baseline() -> dict:
     """The oracle (scalar fp32 per-element dequant, sequential accumulation: the
-    reference gate's algorithm) on one host thread: one full 8B-shape layer at
-    4096 context plus 1/16 of the LM head rows, scaled to a 32-layer step."""
+    reference gate's algorithm) on the host: one full decode step of the
+    32-layer 8B-shape model (embedding row, 32 layers at 4096 context, final
+    norm, Q5_K LM head, argmax) row-parallel on every usable host thread (each
+    row keeps its sequential order, so the outputs equal the 1-thread ones), and
+    one full layer on one thread. Distinct seeded weights per layer, so no
+    layer's 88 MB of packs is cache-resident when the next starts."""
     import ctypes
 
     import numpy as np
@@ -540,56 +587,78 @@ def cpu_baseline() -> dict:
     s = LLAMA_8B
     lib, P = orc.lib(), orc.ptr
     H, q, kv, ff = s.hidden, s.n_heads * HEAD_DIM, s.n_kv_heads * HEAD_DIM, s.ffn
-    qkv = packs.make_pack(F.IQ3S, q + 2 * kv, H, tensor_seed(SEED, 0, "qkv")).payload
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        threads = os.cpu_count() or 1
+    threads = max(1, min(64, threads))
     rb = (H // 256) * 110
-    wq, wk, wv = qkv[:q * rb], qkv[q * rb:(q + kv) * rb], qkv[(q + kv) * rb:]
-    wo = packs.make_pack(F.IQ3S, H, q, tensor_seed(SEED, 0, "o")).payload
-    gu = packs.make_pack(F.IQ2S, 2 * ff, H, tensor_seed(SEED, 0, "gate_up")).payload.reshape(ff, 2, -1)
-    wg, wu = np.ascontiguousarray(gu[:, 0]).ravel(), np.ascontiguousarray(gu[:, 1]).ravel()
-    dn = packs.make_pack(F.Q4K_SPLIT_NATIVE, H, ff, tensor_seed(SEED, 0, "down"))
-    an = packs.normal_f32(SEED + 100, H, mean=1.0, std=0.02)
-    fn = packs.normal_f32(SEED + 101, H, mean=1.0, std=0.02)
-    n = (s.max_ctx // s.page_size) * s.n_kv_heads * s.page_size * HEAD_DIM
-    kc, vc = packs.normal_f16_bits(SEED + 300, n), packs.normal_f16_bits(SEED + 301, n)
-    table = np.arange(s.max_ctx // s.page_size, dtype=np.int32)
     inv_freq = np.empty(HEAD_DIM // 2, np.float32)
     lib.orc_rope_inv_freq(HEAD_DIM, s.rope_theta, P(inv_freq))
-    w = orc.LayerWeights(F.IQ3S, F.IQ3S, F.IQ3S, F.IQ3S, F.IQ2S, F.IQ2S, F.Q4K_SPLIT_NATIVE,
-                         P(wq), None, P(wk), None, P(wv), None, P(wo), None, P(wg), None, P(wu), None,
-                         P(dn.payload), P(dn.meta), P(an), P(fn))
     shape = orc.LayerShape(H, s.n_heads, s.n_kv_heads, HEAD_DIM, ff, s.rms_eps, P(inv_freq))
-    cache = orc.KvCache(P(kc), P(vc), P(table), s.page_size, s.n_kv_heads, HEAD_DIM)
-    rows = s.vocab // 16
-    lm = packs.make_pack(F.Q5K, rows, H, tensor_seed(SEED, None, "lm_head")).payload
+    n = (s.max_ctx // s.page_size) * s.n_kv_heads * s.page_size * HEAD_DIM
+    table = np.arange(s.max_ctx // s.page_size, dtype=np.int32)
+    layers = []
+    for l in range(s.n_layers):
+        qkv = packs.make_pack(F.IQ3S, q + 2 * kv, H, tensor_seed(SEED, l, "qkv")).payload
+        gu = packs.make_pack(F.IQ2S, 2 * ff, H, tensor_seed(SEED, l, "gate_up")).payload.reshape(ff, 2, -1)
+        d = {"wq": qkv[:q * rb], "wk": qkv[q * rb:(q + kv) * rb], "wv": qkv[(q + kv) * rb:],
+             "wo": packs.make_pack(F.IQ3S, H, q, tensor_seed(SEED, l, "o")).payload,
+             "wg": np.ascontiguousarray(gu[:, 0]).ravel(), "wu": np.ascontiguousarray(gu[:, 1]).ravel(),
+             "dn": packs.make_pack(F.Q4K_SPLIT_NATIVE, H, ff, tensor_seed(SEED, l, "down")),
+             "an": packs.normal_f32(SEED + 100 + 2 * l, H, mean=1.0, std=0.02),
+             "fn": packs.normal_f32(SEED + 101 + 2 * l, H, mean=1.0, std=0.02),
+             "kc": packs.normal_f16_bits(SEED + 300 + 2 * l, n), "vc": packs.normal_f16_bits(SEED + 301 + 2 * l, n)}
+        d["w"] = orc.LayerWeights(F.IQ3S, F.IQ3S, F.IQ3S, F.IQ3S, F.IQ2S, F.IQ2S, F.Q4K_SPLIT_NATIVE,
+                                  P(d["wq"]), None, P(d["wk"]), None, P(d["wv"]), None, P(d["wo"]), None, P(d["wg"]),
+                                  None, P(d["wu"]), None, P(d["dn"].payload), P(d["dn"].meta), P(d["an"]), P(d["fn"]))
+        d["cache"] = orc.KvCache(P(d["kc"]), P(d["vc"]), P(table), s.page_size, s.n_kv_heads, HEAD_DIM)
+        layers.append(d)
+    embed = packs.make_pack(F.Q5K, s.vocab, H, tensor_seed(SEED, None, "embed")).payload
+    lm = packs.make_pack(F.Q5K, s.vocab, H, tensor_seed(SEED, None, "lm_head")).payload
+    out_norm = packs.normal_f32(SEED + 99, H, mean=1.0, std=0.02)
+    pos = s.max_ctx - 1
 
-    def step_seconds(threads: int) -> tuple[float, float, float]:
-        h = packs.normal_f32(SEED + 7, H)
-        t0 = time.perf_counter()
-        lib.orc_layer_forward(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(cache), s.max_ctx - 1, P(h),
-                              threads)
-        t_layer = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        orc.matvec_f32(F.Q5K, lm, None, h, rows, H, threads)
-        t_head = (time.perf_counter() - t0) * 16
-        return s.n_layers * t_layer + t_head, t_layer, t_head
+    def layer(l: int, h: np.ndarray, nthreads: int) -> None:
+        d = layers[l]
+        lib.orc_layer_forward(ctypes.byref(d["w"]), ctypes.byref(shape), ctypes.byref(d["cache"]), pos, P(h),
+                              nthreads)
 
-    one, t_layer, t_head = step_seconds(1)
-    # row-parallel: every row keeps its sequential order, so the outputs are the
-    # 1-thread ones; the GPU box gives this process 16 cores
-    n = max(1, min(16, os.cpu_count() or 1))
-    many, m_layer, m_head = step_seconds(n)
-    sample = ("oracle (scalar restatement of the reference CPU gate): one 8B-shape layer at 4096 context and "
-              "1/16 of the Q5_K LM head rows, scaled to 32 layers + full head")
+    # one full layer on one thread (the reference gate's own mode)
+    h1 = packs.normal_f32(SEED + 7, H)
+    t0 = time.perf_counter()
+    layer(0, h1, 1)
+    t_layer1 = time.perf_counter() - t0
+    # the full step on every usable thread
+    t0 = time.perf_counter()
+    h = np.empty(H, np.float32)
+    lib.orc_embed_q5k(P(embed), H, 1234, P(h))
+    t_layers = []
+    for l in range(s.n_layers):
+        tl = time.perf_counter()
+        layer(l, h, threads)
+        t_layers.append(time.perf_counter() - tl)
+    xn = np.empty(H, np.float32)
+    lib.orc_rmsnorm_weighted(P(h), P(out_norm), H, s.rms_eps, P(xn))
+    th = time.perf_counter()
+    logits = orc.matvec_f32(F.Q5K, lm, None, xn, s.vocab, H, threads)
+    t_head = time.perf_counter() - th
+    token = orc.argmax(logits)
+    t_step = time.perf_counter() - t0
+    est1 = s.n_layers * t_layer1 + t_head * threads  # 1-thread step, from the measured layer (head scaled)
     return {
-        "value": round(1.0 / one, 5),
+        "value": round(1.0 / t_step, 5),
         "unit": "tok/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{sample}; 1 thread: layer {t_layer:.2f} s, head/16 {t_head / 16:.2f} s = {one:.1f} s per token",
-        "cpu_model": _cpu_model(),
-        "threads": {"value": round(1.0 / many, 5), "unit": "tok/s", "cores": n, "kind": "port",
-                    "sample": f"{sample}; {n} threads (row-parallel): layer {m_layer:.2f} s, head/16 "
-                              f"{m_head / 16:.2f} s = {many:.1f} s per token"},
+        "sample": (f"oracle (scalar restatement of the reference CPU gate: per-element dequant, sequential fp32 "
+                   f"accumulation) on one full decode step of the 32-layer 8B-shape model at context {pos + 1}: "
+                   f"embedding row, 32 layers (distinct weights), final norm, Q5_K LM head, argmax (token {token}); "
+                   f"{threads} threads row-parallel, {t_step:.1f} s (layers {sum(t_layers):.1f} s, "
+                   f"head {t_head:.2f} s)"),
+        "single_thread": {"layer_s": round(t_layer1, 3), "unit": "s per layer (one full 8B layer, 1 thread)",
+                          "step_estimate_tok_s": round(1.0 / est1, 5)},
+        "host": cpu_info(),
     }
 
 
@@ -635,12 +704,14 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 dot4 (weight codes x 2-digit int8 activation, 15-bit per 16-value group, exact int32 sums) + f32 scales/accumulate",
+        "dtype": "f32 activations staged to 22-bit block fixed point per 16 values (3 int8 digits), exact int32 "
+                 "dot4 with the weight codes, f32 scales and accumulation",
         "data": "synthetic: random-init seeded GGUF packs (splitmix64), norms 1+N(0,0.02), fp16 KV ~ N(0,1)",
         "config": {"workload": "llama-8B-shape decode step: 32 layers (q/k/v/o IQ3_S, gate/up IQ2_S, down Q4_K "
                                "split-native), Q5_K embed + LM head (vocab 128256), GQA 32/8 x 128, "
                                f"paged fp16 KV, context ~{int(dec['mean_context'])}, greedy argmax, one hipGraph",
                    "batch": 1, "launches_per_step": dec["launches"], "wall_s": round(dec["wall_s"], 4)},
+        "latency": dec["latency"],
         "step_hbm_GBps": round(dec["GB/s"], 1),
         "step_frac_of_hbm_peak": round(dec["GB/s"] / HBM_PEAK_GBS, 4),
         "step_algorithmic_bytes": int(dec["step_bytes"]),
@@ -657,7 +728,7 @@ def main() -> int:
             "workload": "the same decode step for 8 sequences at once (one pass over the weights on the matrix "
                         "cores, every sequence with its own token, position and KV pages, context ~"
                         f"{int(b8['mean_context'])} each), one hipGraph",
-            "tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 5),
+            "tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 5), "latency": b8["latency"],
             "step_hbm_GBps": round(b8["GB/s"], 1), "step_frac_of_hbm_peak": round(b8["GB/s"] / HBM_PEAK_GBS, 4),
             "step_algorithmic_bytes": int(b8["step_bytes"]), "launches_per_step": b8["launches"],
             "dtype": "fp16 weight codes x sub-block scale (exact) times hi+lo fp16 activations on the matrix "

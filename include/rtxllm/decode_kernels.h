@@ -10,11 +10,33 @@
  *
  * The rtxllm_* entry points without "launch" in their names have no
  * counterpart in the reference; they carry the math of a real Llama decode step
- * (pure y = W x on an fp32 or a staged activation) and the host-side pack
- * helpers; the Llama layer math (weighted RMSNorm, RoPE with a theta schedule,
- * SiLU-gate multiply, Q5_K embedding gather, GQA attention over a paged fp16
- * KV cache, greedy argmax) is reached through the decode runner of
- * rtxllm/llama.h.
+ * (pure y = W x on an fp32 or a staged activation, batched matvecs, weighted
+ * RMSNorm, RoPE with a theta schedule, SiLU-gate multiply, Q5_K embedding
+ * gather, GQA attention over a paged fp16 KV cache, greedy argmax) and the
+ * host-side pack helpers. The decode runner of rtxllm/llama.h fuses the same
+ * math into its matvec epilogues.
+ *
+ * Activation precision of every batch-1 matvec (the reference-named launchers
+ * included): the kernels multiply the weight codes with the fp32 activation
+ * through exact integer dot products after staging x per 16-value group as
+ * 22-bit block fixed point (see rtxllm_stage_activation): each value is
+ * rounded once, to a multiple of s = 2^(e - 22) where max|x| of its group is in
+ * [2^(e-1), 2^e), so its error is at most 2^-23 of the group maximum. A
+ * 4096-column product then stays closer to the exact (float64) result than
+ * the reference's fp32 sequential accumulation (main.cpp:1261-1309) does, also
+ * for groups with outliers. A NaN activation makes its group's scale NaN, so
+ * the outputs become NaN as in fp32; an infinite one makes them NaN where fp32
+ * gives +-inf or NaN.
+ *
+ * Pointer alignment: activation pointers (x, activation) may have any 4-byte
+ * alignment. Weight streams must be aligned as the kernels' vector loads need
+ * them (the reference's vec4x4 kernels likewise read 16-byte float4 of x and
+ * 4-byte words of the payload, decode_kernels.cu:2893-2991): Q4_K payloads and
+ * predecoded / native metadata, Q5_K blocks and the IQ2S_UNITS / IQ3S_UNITS
+ * layouts 16 bytes, split-half metadata 8, split-compact metadata 4, IQ2_S /
+ * IQ3_S blocks 2. A misaligned weight pointer is refused with
+ * hipErrorInvalidValue. The staged buffers (xq, x16) and workspaces are 16-byte
+ * aligned (256 for the attention workspace).
  *
  * Pack layouts (all row-major, rows x (cols / 256) blocks, cols % 256 == 0):
  *   Q4_K raw 144 B, Q5_K 176 B, IQ2_S 82 B, IQ3_S 110 B GGUF blocks;
@@ -196,19 +218,20 @@ hipError_t rtxllm_dequant_f32(int format, const uint8_t* payload, const uint8_t*
                               uint32_t cols, float* out, hipStream_t stream);
 
 /* y[rows] = W x (batch 1), no side effects. x is fp32; each wave stages the
- * columns it owns itself (see rtxllm_stage_activation for the staging rule). */
+ * columns it owns itself (the rtxllm_stage_activation rule). */
 hipError_t rtxllm_matvec(int format, const uint8_t* payload, const uint8_t* meta, const float* x, float* y,
                          uint32_t rows, uint32_t cols, hipStream_t stream);
 
-/* Staged activation ("xq"): x is cut into 16-value groups; each group is kept as
- * 15-bit fixed point X_j = rint(x_j * K / max|x|), K = 127 * 256 = 32512,
- * split into two int8 digits X_j = 256 H_j + L_j (H in [-127, 127], L in
- * [-128, 127]), plus the group scale s = max|x| / K and the group sum
- * s * sum(X). Layout of one buffer of rtxllm_xq_bytes(cols) bytes: H[cols],
+/* Staged activation ("xq"): x is cut into 16-value groups. For a group with
+ * maximum magnitude m = f 2^e (f in [0.5, 1)) the scale is s = 2^(e - 22) and
+ * each value is held as X_j = rint(x_j 2^(22 - e)) (|X_j| <= 2^22, so x_j =
+ * s X_j up to s / 2), split into three int8 digits X_j = 65536 H_j + 256 M_j +
+ * L_j (H in [-64, 64], M and L in [-128, 127]), plus the group scale s and the
+ * group sum s * sum(X). A group holding a NaN has s = NaN, one whose maximum
+ * is infinite s = inf (all digits 0); an all-zero group s = 0. Layout of one
+ * buffer of rtxllm_xq_bytes(cols) bytes (16-byte aligned): H[cols], M[cols],
  * L[cols] (int8), s[cols/16], sum[cols/16] (f32). The matvec kernels multiply
- * the weight codes with the digits through exact integer dot products, so the
- * staging rounding (a step of 3.1e-5 of the group maximum) is the only
- * deviation from an fp32 product. */
+ * the weight codes with the digits through exact integer dot products. */
 size_t rtxllm_xq_bytes(uint32_t cols);
 /* xq = stage(x * weight) (weight may be null: stage x). cols % 256 == 0. */
 hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t cols, void* xq,
@@ -248,12 +271,52 @@ hipError_t rtxllm_matvec_batch_f32(int format, const uint8_t* payload, const uin
                                    float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
                                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Measurement helper, no counterpart in the reference: a plain streaming read
- * of `bytes` (a multiple of 16, 16-byte aligned) by `workgroups` workgroups of
- * 256 threads, each writing the xor of what it read to out[workgroup]. bench.py
- * times it over the decode stages' byte counts as the practical HBM ceiling. */
-hipError_t rtxllm_stream_read(const void* data, size_t bytes, uint32_t* out, uint32_t workgroups,
-                              hipStream_t stream);
+/* ---- Llama layer math (no counterpart in the reference; its stages are
+ * composed from separate launchers the same way, decode_kernels.h:38-101,
+ * 319-325, main.cpp:4073-4279). All asynchronous on `stream`. ---- */
+
+/* out[r] = (x[r] * inv_rms) * weight (weight null: no weight), inv_rms = 1 /
+ * sqrt(sum(x[r]^2) / n + eps), for count vectors x [count][n] (in place
+ * allowed). */
+hipError_t rtxllm_rmsnorm_w(const float* x, const float* weight, uint32_t n, uint32_t count, float eps,
+                            float* out, hipStream_t stream);
+
+/* In place on vec [count][n_heads][head_dim] (8-byte aligned): each adjacent
+ * pair (2i, 2i+1) of every head of vector r rotated by the angle pos[r] *
+ * theta^(-2i / head_dim) (pos a device array of count positions):
+ * (e, o) -> (e cos - o sin, e sin + o cos). head_dim even. */
+hipError_t rtxllm_rope_theta(float* vec, uint32_t n_heads, uint32_t head_dim, float theta, const uint32_t* pos,
+                             uint32_t count, hipStream_t stream);
+
+/* out[i] = silu(gate[i]) * up[i], silu(v) = v / (1 + exp(-v)) (in place allowed). */
+hipError_t rtxllm_silu_mul(const float* gate, const float* up, size_t n, float* out, hipStream_t stream);
+
+/* out[t][cols] = the Q5_K row tokens[t] of table [vocab][cols / 256 blocks]
+ * dequantised (bit-exact with the reference's Q5_K formula, main.cpp:1231-1259),
+ * for count device token ids; a token >= vocab gives a row of NaN. table
+ * 4-byte aligned. */
+hipError_t rtxllm_embed_gather_q5k(const uint8_t* table, uint32_t vocab, uint32_t cols, const uint32_t* tokens,
+                                   uint32_t count, float* out, hipStream_t stream);
+
+/* GQA decode attention of count queries (head_dim 128): q [count][n_heads][128]
+ * fp32; query head h reads kv head h / (n_heads / n_kv_heads) (group 1, 2, 4
+ * or 8); K and V fp16 caches of pages [page][n_kv_heads][page_size][128]
+ * (16-byte aligned); query r attends positions 0..pos[r] (pos a device array,
+ * pos[r] < capacity) through block-table row r (table_stride entries apart,
+ * capacity / page_size entries used: logical page -> physical page); scores
+ * scaled by 1 / sqrt(128), softmax with the maximum subtracted; out [count]
+ * [n_heads][128] fp32. workspace: rtxllm_attn_decode_workspace() bytes. */
+size_t rtxllm_attn_decode_workspace(uint32_t n_heads, uint32_t n_kv_heads, uint32_t capacity, uint32_t count);
+hipError_t rtxllm_attn_decode_gqa_f16(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                      const int32_t* block_table, uint32_t table_stride, uint32_t n_heads,
+                                      uint32_t n_kv_heads, uint32_t page_size, uint32_t capacity,
+                                      const uint32_t* pos, uint32_t count, float* out, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream);
+
+/* index[r] = argmax of x [count][n] row r: the lowest index among equal maxima;
+ * the scan starts from (-FLT_MAX, 0) as the reference's (decode_kernels.cu:
+ * 2993-3031), so a NaN never wins and a row with nothing above -FLT_MAX gives 0. */
+hipError_t rtxllm_argmax(const float* x, uint32_t n, uint32_t count, uint32_t* index, hipStream_t stream);
 
 /* GGUF IQ2_S blocks (format 6) of a rows x cols tensor -> the same bytes in the
  * IQ2S_UNITS layout (format 9), device to device: per 32-value unit k of block b

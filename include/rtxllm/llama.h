@@ -61,6 +61,7 @@ void rtxllm_llama_destroy(rtxllm_llama* m);
  * "k_cache", "v_cache" (fp16 [pages][n_kv][page_size][128]), "block_table"
  * (int32 [max_ctx / page_size]). Global (layer ignored): "embed", "lm_head",
  * "lm_head_meta", "out_norm", "h", "q", "att", "act", "logits", "token", "pos",
+ * "status",
  * and the work buffers "xq" / "xq_att" (staged activations), "sumsq",
  * "attn_partials", "argkeys", "inv_freq", "rope" ((cos, sin) of every
  * position's rotary angles, float2 [max_ctx][64]); with batch > 1 also "x16" (staged
@@ -87,7 +88,9 @@ void* rtxllm_llama_region(rtxllm_llama* m, const char* name, uint32_t layer, siz
 void rtxllm_llama_weights_changed(rtxllm_llama* m);
 
 /* Synchronous host <-> region copies (setup and inspection; not capture-safe):
- * `bytes` at byte `offset` of the region. hipErrorInvalidValue if out of range. */
+ * `bytes` at byte `offset` of the region. hipErrorInvalidValue if out of range,
+ * and for an upload to "pos" (or "token") of a value >= max_ctx (>= vocab):
+ * a position must have a KV slot, a token an embedding row. */
 hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset, const void* src,
                                size_t bytes);
 hipError_t rtxllm_llama_download(rtxllm_llama* m, const char* name, uint32_t layer, size_t offset, void* dst,
@@ -109,7 +112,9 @@ hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_
  * output (".weight"). Each must be in the configured format (a Q4_K split
  * layout's pack policy must match it; raw Q4_K comes from blocks_path) with
  * the model's shape, and every file's size and byte-sum checksum must match
- * its manifest. hipErrorInvalidValue with the reason in err otherwise. */
+ * its manifest. hipErrorInvalidValue with the reason in err otherwise; every
+ * tensor is read and checked before the first upload, so a refused pack set
+ * leaves the model's weights as they were. */
 hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_manifest, const char* iq_manifest,
                                    const char* payload_root, char* err, size_t err_len);
 
@@ -150,6 +155,18 @@ size_t rtxllm_llama_graph_bytes(const rtxllm_llama* m);
 hipError_t rtxllm_llama_launch_stage(rtxllm_llama* m, uint32_t layer, int stage, hipStream_t stream);
 /* Kernel launches per decode step. */
 uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m);
+
+/* Per-sequence status words (region "status", uint32 [batch], 0 at create).
+ * RTXLLM_LLAMA_STATUS_CONTEXT_FULL: a step ran while the sequence's position
+ * was max_ctx (its KV cache full): that step had no slot for its token, so it
+ * left the sequence's token and position as they were (the sequence halts at
+ * max_ctx instead of decoding past the context end). The bit stays set until
+ * cleared. rtxllm_llama_status copies the batch's words to host memory and
+ * waits for the stream; rtxllm_llama_clear_status zeroes them (both
+ * synchronous, not capture-safe). */
+enum { RTXLLM_LLAMA_STATUS_CONTEXT_FULL = 1 };
+hipError_t rtxllm_llama_status(rtxllm_llama* m, uint32_t* status, hipStream_t stream);
+hipError_t rtxllm_llama_clear_status(rtxllm_llama* m, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,10 +1,15 @@
-// Measurement helper: a plain streaming read of a device buffer, the practical
-// HBM ceiling the decode kernels are compared with (bench.py --read-ceiling).
+// Measurement helper, not part of the decode library: a plain streaming read of
+// a device buffer, the practical HBM ceiling the decode kernels are compared
+// with (bench.py --read-ceiling). Built into its own build/librtxllm_probe.so.
+//
+// extern "C" hipError_t rtxllm_stream_read(const void* data, size_t bytes,
+//     uint32_t* out, uint32_t workgroups, hipStream_t stream): read `bytes` (a
+//     multiple of 16, 16-byte aligned) with `workgroups` workgroups of 256
+//     threads, each writing the xor of what it read to out[workgroup].
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
-
-#include "rtxllm/decode_kernels.h"
 
 namespace rtxllm {
 namespace {

@@ -96,13 +96,21 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
                          std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* keys,
                          std::uint32_t key_capacity, std::uint32_t* key_count, hipStream_t stream);
 
-// token[0] = argmax over keys[0, count) (0 if every logit was NaN); *pos += advance.
+// Status bit of a sequence whose step ran at a position >= the KV capacity.
+constexpr std::uint32_t kStatusContextFull = 1u;
+
+// token[0] = argmax over keys[0, count) (0 if every logit was NaN); *pos +=
+// advance; but when *pos >= capacity (the step had no KV slot) token and pos
+// stay and *status |= kStatusContextFull (status may be null).
 hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
-                                  std::uint32_t* pos, std::uint32_t advance, hipStream_t stream);
-// The same per sequence s < batch over keys[s * key_stride, + count): token[s], pos[s].
+                                  std::uint32_t* pos, std::uint32_t advance, std::uint32_t capacity,
+                                  std::uint32_t* status, hipStream_t stream);
+// The same per sequence s < batch over keys[s * key_stride, + count): token[s],
+// pos[s], status[s].
 hipError_t launch_argmax_finalize_batch(const unsigned long long* keys, std::uint32_t key_stride,
                                         std::uint32_t count, std::uint32_t batch, std::uint32_t* token,
-                                        std::uint32_t* pos, std::uint32_t advance, hipStream_t stream);
+                                        std::uint32_t* pos, std::uint32_t advance, std::uint32_t capacity,
+                                        std::uint32_t* status, hipStream_t stream);
 
 // ---- batch (2..8 sequences) step, on the matrix cores (batch.hip) ------------
 // x16: a staged batch activation (rtxllm_x16_bytes); columns of sequences >=

@@ -58,21 +58,21 @@ __device__ __forceinline__ float inv_rms(const float* __restrict__ sumsq, std::u
 __device__ __forceinline__ void stage_group16(const XQOut& xq, std::uint32_t g0, std::uint32_t idx, float x,
                                               bool owner, std::uint32_t lane) {
   const float m = wave_max(fabsf(x));
-  const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
-  const float s = m / kXQLimitF;
-  int X = static_cast<int>(rintf(x * inv));
-  X = X > kXQLimit ? kXQLimit : (X < -kXQLimit ? -kXQLimit : X);
-  int H, L;
-  xq_digits(X, H, L);
+  const bool nan = __ballot(owner && x != x) != 0ull;
+  const XScale sc = xq_scale(m, nan);
+  const int X = xq_fixed(x, sc);
+  int H, M, L;
+  xq_digits(X, H, M, L);
   const int total = wave_sum_i(owner ? X : 0);
   if (owner) {
     xq.h[idx] = static_cast<std::int8_t>(H);
+    xq.m[idx] = static_cast<std::int8_t>(M);
     xq.l[idx] = static_cast<std::int8_t>(L);
   }
   if (lane == 0u) {
     const std::uint32_t t = g0 / kXGroup;
-    xq.s[t] = s;
-    xq.sum[t] = s * static_cast<float>(total);
+    xq.s[t] = sc.s;
+    xq.sum[t] = sc.s * static_cast<float>(total);
   }
 }
 
@@ -482,14 +482,15 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   m = fmaxf(m, __shfl_xor(m, 1, 64));
   m = fmaxf(m, __shfl_xor(m, 2, 64));
   m = fmaxf(m, __shfl_xor(m, 4, 64));
-  const float inv = m > 0.0f ? kXQLimitF / m : 0.0f;
-  const float s = m / kXQLimitF;
-  int X0 = static_cast<int>(rintf(a0 * inv)), X1 = static_cast<int>(rintf(a1 * inv));
-  X0 = X0 > kXQLimit ? kXQLimit : (X0 < -kXQLimit ? -kXQLimit : X0);
-  X1 = X1 > kXQLimit ? kXQLimit : (X1 < -kXQLimit ? -kXQLimit : X1);
-  int H0, L0, H1, L1;
-  xq_digits(X0, H0, L0);
-  xq_digits(X1, H1, L1);
+  int nan = __builtin_isunordered(a0, a1) ? 1 : 0;
+  nan |= __shfl_xor(nan, 1, 64);
+  nan |= __shfl_xor(nan, 2, 64);
+  nan |= __shfl_xor(nan, 4, 64);
+  const XScale sc = xq_scale(m, nan != 0);
+  const int X0 = xq_fixed(a0, sc), X1 = xq_fixed(a1, sc);
+  int H0, M0, L0, H1, M1, L1;
+  xq_digits(X0, H0, M0, L0);
+  xq_digits(X1, H1, M1, L1);
   int total = X0 + X1;
   total += __shfl_xor(total, 1, 64);
   total += __shfl_xor(total, 2, 64);
@@ -499,11 +500,12 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
                                       ((static_cast<std::uint32_t>(hi) & 0xFFu) << 8));
   };
   *reinterpret_cast<std::uint16_t*>(xq.h + d0) = pair(H0, H1);
+  *reinterpret_cast<std::uint16_t*>(xq.m + d0) = pair(M0, M1);
   *reinterpret_cast<std::uint16_t*>(xq.l + d0) = pair(L0, L1);
   if ((lane & 7u) == 0u) {
     const std::uint32_t t = d0 / kXGroup;
-    xq.s[t] = s;
-    xq.sum[t] = s * static_cast<float>(total);
+    xq.s[t] = sc.s;
+    xq.sum[t] = sc.s * static_cast<float>(total);
   }
 }
 
@@ -555,15 +557,19 @@ __global__ __launch_bounds__(128) void attn_combine_x16_kernel(const float* __re
 }
 
 // One workgroup of 256 per sequence (blockIdx.x, keys key_stride apart): the
-// maximum of count keys, then token and position.
+// maximum of count keys, then token and position. A step that ran at a
+// position >= capacity had no KV slot for its token: its token and position
+// are left as they were and status gets kStatusContextFull.
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
                                                               std::uint32_t count, std::uint32_t* token,
                                                               std::uint32_t* pos, std::uint32_t advance,
-                                                              std::uint32_t key_stride) {
+                                                              std::uint32_t key_stride, std::uint32_t capacity,
+                                                              std::uint32_t* status) {
   __shared__ unsigned long long part[4];
   keys += static_cast<std::size_t>(blockIdx.x) * key_stride;
   token += blockIdx.x;
   if (pos != nullptr) pos += blockIdx.x;
+  if (status != nullptr) status += blockIdx.x;
   unsigned long long best = 0ull;
   for (std::uint32_t i0 = threadIdx.x; i0 < count; i0 += 256u * 8u) {
     unsigned long long k[8];
@@ -584,6 +590,10 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
   __syncthreads();
   if (threadIdx.x != 0u) return;
   for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
+  if (pos != nullptr && pos[0] >= capacity) {
+    if (status != nullptr) status[0] |= kStatusContextFull;
+    return;
+  }
   token[0] = best == 0ull ? 0u : 0xFFFFFFFFu - static_cast<std::uint32_t>(best & 0xFFFFFFFFull);
   if (pos != nullptr) pos[0] += advance;
 }
@@ -633,7 +643,7 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
   e.q_rows = q_rows, e.kv_rows = kv_rows, e.rope = rope, e.rope_positions = rope_positions;
   e.group = q_rows / kHeadDim / kv.n_kv;
   e.pos_ptr = pos, e.q = static_cast<_Float16*>(q_out), e.kv = kv;
-  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, w.rows, e, stream);
+  return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), w.rows, e, stream);
 }
 
 std::size_t attention_partials_floats(std::uint32_t n_heads, std::uint32_t n_kv, std::uint32_t span) {
@@ -697,8 +707,8 @@ hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint
   if ((rows % kXGroup) != 0u || (xq_in == nullptr) == (x_in == nullptr)) return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   const EpiResidual e{h, w_next, xq_out(xq_next, rows), sumsq_next};
-  if (xq_in != nullptr) return launch_mv<false>(fmt, w, XSrc{xq_view(xq_in, cols), nullptr}, rows, e, stream);
-  return launch_mv<true>(fmt, w, XSrc{XQ{}, x_in}, rows, e, stream);
+  if (xq_in != nullptr) return launch_mv<false>(fmt, w, staged_src(xq_view(xq_in, cols)), rows, e, stream);
+  return launch_mv<true>(fmt, w, self_src(x_in), rows, e, stream);
 }
 
 hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
@@ -707,7 +717,7 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
   const QTensor w{payload, meta, rows, cols};
   EpiGateUp e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.act = act;
-  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
+  return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, e, stream);
 }
 
 std::uint32_t logits_key_slots(int fmt, std::uint32_t rows, std::uint32_t cols) {
@@ -725,21 +735,23 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
   const QTensor w{payload, meta, rows, cols};
   EpiLogits e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.logits = logits, e.keys = keys;
-  return launch_mv<false>(fmt, w, XSrc{xq_view(in.xq, cols), nullptr}, rows, e, stream);
+  return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, e, stream);
 }
 
 hipError_t launch_argmax_finalize(const unsigned long long* keys, std::uint32_t count, std::uint32_t* token,
-                                  std::uint32_t* pos, std::uint32_t advance, hipStream_t stream) {
-  return launch_argmax_finalize_batch(keys, 0u, count, 1u, token, pos, advance, stream);
+                                  std::uint32_t* pos, std::uint32_t advance, std::uint32_t capacity,
+                                  std::uint32_t* status, hipStream_t stream) {
+  return launch_argmax_finalize_batch(keys, 0u, count, 1u, token, pos, advance, capacity, status, stream);
 }
 
 hipError_t launch_argmax_finalize_batch(const unsigned long long* keys, std::uint32_t key_stride,
                                         std::uint32_t count, std::uint32_t batch, std::uint32_t* token,
-                                        std::uint32_t* pos, std::uint32_t advance, hipStream_t stream) {
+                                        std::uint32_t* pos, std::uint32_t advance, std::uint32_t capacity,
+                                        std::uint32_t* status, hipStream_t stream) {
   if (keys == nullptr || token == nullptr || batch == 0u || (batch > 1u && key_stride < count))
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(batch), dim3(256), 0, stream, keys, count, token, pos, advance,
-                     key_stride);
+                     key_stride, capacity, status);
   return hipGetLastError();
 }
 

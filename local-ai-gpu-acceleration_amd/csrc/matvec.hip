@@ -16,10 +16,12 @@ bool aligned(const void* p, std::uintptr_t a) { return (reinterpret_cast<std::ui
 
 bool shape_ok(std::uint32_t rows, std::uint32_t cols) { return rows != 0u && cols != 0u && (cols % 256u) == 0u; }
 
-// The kernels issue 16-byte loads of x, of 16-byte aligned block fields and of
-// the Q4_K metadata records; reject pointers that break those alignments.
-bool pointers_ok(int fmt, const void* payload, const void* meta, const void* x) {
-  if (x != nullptr && !aligned(x, 16)) return false;
+// The kernels issue 16-byte loads of 16-byte aligned block fields and of the
+// Q4_K metadata records; reject weight pointers that break those alignments.
+// An fp32 activation may have any 4-byte alignment (the kernels stage a
+// misaligned one value by value); a staged activation is 16-byte aligned.
+bool pointers_ok(int fmt, const void* payload, const void* meta, const void* x, bool staged = false) {
+  if (x != nullptr && !aligned(x, staged ? 16 : 4)) return false;
   const bool iq = fmt == RTXLLM_FMT_IQ2S || fmt == RTXLLM_FMT_IQ3S;  // IQ2S_UNITS: 16 (8-byte field loads)
   if (!aligned(payload, iq ? 2 : 16)) return false;
   if (needs_meta(fmt)) {
@@ -110,7 +112,7 @@ hipError_t decode_call(int fmt, const std::uint8_t* payload, const std::uint8_t*
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   const EpiDecode<kTile> epi{y, kv, token, kv_words, page_words, active_pages};
-  const hipError_t st = launch_mv<true>(fmt, w, XSrc{XQ{}, x}, launched_rows, epi, stream);
+  const hipError_t st = launch_mv<true>(fmt, w, self_src(x), launched_rows, epi, stream);
   if (st != hipSuccess) return st;
   return launch_argmax_token(y, token, launched_rows, 0, 32000u, 0u, stream);
 }
@@ -172,7 +174,7 @@ extern "C" hipError_t rtxllm_matvec(int format, const std::uint8_t* payload, con
       (needs_meta(format) && meta == nullptr) || !pointers_ok(format, payload, meta, x))
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
-  return launch_mv<true>(format, w, XSrc{XQ{}, x}, rows, EpiStore<kTile>{y}, stream);
+  return launch_mv<true>(format, w, self_src(x), rows, EpiStore<kTile>{y}, stream);
 }
 
 extern "C" std::size_t rtxllm_xq_bytes(std::uint32_t cols) { return xq_bytes(cols); }
@@ -181,10 +183,10 @@ extern "C" hipError_t rtxllm_matvec_xq(int format, const std::uint8_t* payload, 
                                        const void* xq, float* y, std::uint32_t rows, std::uint32_t cols,
                                        hipStream_t stream) {
   if (!shape_ok(rows, cols) || payload == nullptr || xq == nullptr || y == nullptr ||
-      (needs_meta(format) && meta == nullptr) || !pointers_ok(format, payload, meta, xq))
+      (needs_meta(format) && meta == nullptr) || !pointers_ok(format, payload, meta, xq, true))
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
-  return launch_mv<false>(format, w, XSrc{xq_view(xq, cols), nullptr}, rows, EpiStore<kTile>{y}, stream);
+  return launch_mv<false>(format, w, staged_src(xq_view(xq, cols)), rows, EpiStore<kTile>{y}, stream);
 }
 
 // ---- reference-named matvec launchers --------------------------------------
@@ -285,6 +287,6 @@ extern "C" hipError_t rtxllm_launch_iq2s_matvec_probe(const std::uint8_t* iq2s_b
       logits == nullptr || !pointers_ok(RTXLLM_FMT_IQ2S, iq2s_blocks, nullptr, activation))
     return hipErrorInvalidValue;
   const QTensor w{iq2s_blocks, nullptr, rows, cols};
-  return launch_mv<true>(RTXLLM_FMT_IQ2S, w, XSrc{XQ{}, activation}, clip_rows(rows, rows_limit),
+  return launch_mv<true>(RTXLLM_FMT_IQ2S, w, self_src(activation), clip_rows(rows, rows_limit),
                          EpiStore<kTile>{logits}, stream);
 }

@@ -249,6 +249,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
   specs.push_back({"argkeys", 8u * B * m->key_slots});
   specs.push_back({"token", 4u * B});
   specs.push_back({"pos", 4u * B});
+  specs.push_back({"status", 4u * B});
   if (batch > 1u) {
     const std::uint32_t widest = std::max({c.hidden, m->q_rows, c.ffn});
     specs.push_back({"x16", rtxllm_x16_bytes(widest)});
@@ -376,6 +377,17 @@ extern "C" hipError_t rtxllm_llama_upload(rtxllm_llama* m, const char* name, uin
   std::size_t size = 0;
   auto* base = static_cast<std::uint8_t*>(rtxllm_llama_region(m, name, layer, &size));
   if (base == nullptr || src == nullptr || offset > size || bytes > size - offset) return hipErrorInvalidValue;
+  // positions must have a KV slot and tokens a row of the embedding table
+  const std::string key = name;
+  if (key == "pos" || key == "token") {
+    if (offset % 4u != 0u || bytes % 4u != 0u) return hipErrorInvalidValue;
+    const std::uint32_t limit = key == "pos" ? m->cfg.max_ctx : m->cfg.vocab;
+    for (std::size_t i = 0; i < bytes / 4u; ++i) {
+      std::uint32_t v;
+      std::memcpy(&v, static_cast<const std::uint8_t*>(src) + 4u * i, 4u);
+      if (v >= limit) return hipErrorInvalidValue;
+    }
+  }
   const int u = unit_copy(m, name);
   if (u >= 0) m->units_dirty[static_cast<std::size_t>(u) * m->cfg.n_layers + layer] = 1;
   return hipMemcpy(base + offset, src, bytes, hipMemcpyHostToDevice);
@@ -507,50 +519,65 @@ extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_m
         throw std::runtime_error("tensor shape disagrees with the model: " + name);
       return it->second;
     };
-    auto put = [&](const std::string& region, const std::vector<std::uint8_t>& bytes) {
-      if (bytes.empty()) return;
+    // Every upload is planned and checked first (tensor present, shape, region
+    // size), then performed: a refused pack set leaves the weights untouched.
+    struct Upload {
+      std::string region;
+      std::vector<const std::vector<std::uint8_t>*> parts;  // stacked in order
+      std::size_t interleave_rows;                         // > 0: parts[0], parts[1] interleaved by row
+    };
+    std::vector<Upload> plan;
+    auto add = [&](const std::string& region, std::vector<const std::vector<std::uint8_t>*> parts,
+                   std::size_t rows = 0) {
+      std::size_t bytes = 0;
+      for (const auto* p : parts) bytes += p->size();
+      if (bytes == 0) return;  // no metadata stream for this format
       std::size_t size = 0;
-      void* dst = rtxllm_llama_region(m, region.c_str(), 0u, &size);
-      if (dst == nullptr || size != bytes.size()) throw std::runtime_error("region size mismatch: " + region);
-      const hipError_t st = hipMemcpy(dst, bytes.data(), bytes.size(), hipMemcpyHostToDevice);
-      if (st != hipSuccess) throw std::runtime_error(std::string("upload failed: ") + hipGetErrorString(st));
-      mark_units_dirty(m);
-    };
-    // stack rows (q | k | v) or interleave them (gate_i, up_i) stream by stream
-    auto stack = [](std::initializer_list<const std::vector<std::uint8_t>*> parts) {
-      std::vector<std::uint8_t> out;
-      for (const auto* p : parts) out.insert(out.end(), p->begin(), p->end());
-      return out;
-    };
-    auto interleave = [](const std::vector<std::uint8_t>& a, const std::vector<std::uint8_t>& b, std::size_t rows) {
-      std::vector<std::uint8_t> out(a.size() + b.size());
-      if (rows == 0 || a.size() != b.size() || a.size() % rows != 0) throw std::runtime_error("gate/up streams differ");
-      const std::size_t rb = a.size() / rows;
-      for (std::size_t i = 0; i < rows; ++i) {
-        std::memcpy(out.data() + (2 * i) * rb, a.data() + i * rb, rb);
-        std::memcpy(out.data() + (2 * i + 1) * rb, b.data() + i * rb, rb);
-      }
-      return out;
+      if (rtxllm_llama_region(m, region.c_str(), 0u, &size) == nullptr || size != bytes)
+        throw std::runtime_error("region size mismatch: " + region);
+      if (rows > 0 && (parts.size() != 2 || parts[0]->size() != parts[1]->size() || parts[0]->size() % rows != 0))
+        throw std::runtime_error("gate/up streams differ: " + region);
+      plan.push_back({region, std::move(parts), rows});
     };
     for (std::uint32_t l = 0; l < c.n_layers; ++l) {
       const std::string b = "blk." + std::to_string(l) + ".", L = "L" + std::to_string(l) + ".";
       const auto &q = get(b + "attn_q.weight"), &k = get(b + "attn_k.weight"), &v = get(b + "attn_v.weight");
-      put(L + "qkv", stack({&q.payload, &k.payload, &v.payload}));
-      put(L + "qkv_meta", stack({&q.meta, &k.meta, &v.meta}));
+      add(L + "qkv", {&q.payload, &k.payload, &v.payload});
+      add(L + "qkv_meta", {&q.meta, &k.meta, &v.meta});
       const auto& o = get(b + "attn_output.weight");
-      put(L + "o", o.payload);
-      put(L + "o_meta", o.meta);
+      add(L + "o", {&o.payload});
+      add(L + "o_meta", {&o.meta});
       const auto &g = get(b + "ffn_gate.weight"), &u = get(b + "ffn_up.weight");
-      put(L + "gate_up", interleave(g.payload, u.payload, F));
-      if (!g.meta.empty()) put(L + "gate_up_meta", interleave(g.meta, u.meta, F));
+      add(L + "gate_up", {&g.payload, &u.payload}, F);
+      add(L + "gate_up_meta", {&g.meta, &u.meta}, F);
       const auto& d = get(b + "ffn_down.weight");
-      put(L + "down", d.payload);
-      put(L + "down_meta", d.meta);
+      add(L + "down", {&d.payload});
+      add(L + "down_meta", {&d.meta});
     }
-    put("embed", get("token_embd.weight").payload);
+    add("embed", {&get("token_embd.weight").payload});
     const auto& lm = get("output.weight");
-    put("lm_head", lm.payload);
-    put("lm_head_meta", lm.meta);
+    add("lm_head", {&lm.payload});
+    add("lm_head_meta", {&lm.meta});
+    // stack rows (q | k | v) or interleave them (gate_i, up_i) stream by stream
+    std::vector<std::uint8_t> staging;
+    mark_units_dirty(m);
+    for (const Upload& up : plan) {
+      staging.clear();
+      if (up.interleave_rows > 0) {
+        const auto &a = *up.parts[0], &bb = *up.parts[1];
+        const std::size_t rb = a.size() / up.interleave_rows;
+        staging.resize(a.size() + bb.size());
+        for (std::size_t i = 0; i < up.interleave_rows; ++i) {
+          std::memcpy(staging.data() + (2 * i) * rb, a.data() + i * rb, rb);
+          std::memcpy(staging.data() + (2 * i + 1) * rb, bb.data() + i * rb, rb);
+        }
+      } else {
+        for (const auto* p : up.parts) staging.insert(staging.end(), p->begin(), p->end());
+      }
+      void* dst = rtxllm_llama_region(m, up.region.c_str(), 0u, nullptr);
+      const hipError_t st = hipMemcpy(dst, staging.data(), staging.size(), hipMemcpyHostToDevice);
+      if (st != hipSuccess) throw std::runtime_error(std::string("upload failed: ") + hipGetErrorString(st));
+    }
   } catch (const std::exception& e) {
     report(e.what());
     return hipErrorInvalidValue;
@@ -651,7 +678,8 @@ hipError_t launch_stage_batch(rtxllm_llama* m, std::uint32_t l, int stage, bool 
                                                            B, region<float>(m, "logits"), keys, m->key_slots, &count,
                                                            stream);
       if (st != hipSuccess) return st;
-      return rtxllm::launch_argmax_finalize_batch(keys, m->key_slots, count, B, token, pos, 1u, stream);
+      return rtxllm::launch_argmax_finalize_batch(keys, m->key_slots, count, B, token, pos, 1u, c.max_ctx,
+                                                  region<std::uint32_t>(m, "status"), stream);
     }
     default: return hipErrorInvalidValue;
   }
@@ -708,7 +736,8 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
       const hipError_t st = rtxllm::launch_logits(c.fmt_lm_head, t.payload, t.meta, c.vocab, c.hidden, in,
                                                   region<float>(m, "logits"), keys, m->key_slots, &count, stream);
       if (st != hipSuccess) return st;
-      return rtxllm::launch_argmax_finalize(keys, count, region<std::uint32_t>(m, "token"), pos, 1u, stream);
+      return rtxllm::launch_argmax_finalize(keys, count, region<std::uint32_t>(m, "token"), pos, 1u, c.max_ctx,
+                                            region<std::uint32_t>(m, "status"), stream);
     }
     default: return hipErrorInvalidValue;
   }
@@ -879,4 +908,18 @@ extern "C" hipError_t rtxllm_llama_graph_replay(rtxllm_llama* m, hipStream_t str
     return hipErrorLaunchFailure;
   }
   return hipSuccess;
+}
+
+extern "C" hipError_t rtxllm_llama_status(rtxllm_llama* m, uint32_t* status, hipStream_t stream) {
+  if (m == nullptr || status == nullptr) return hipErrorInvalidValue;
+  hipError_t st = hipMemcpyAsync(status, m->arena.arena_ptr("status"), 4u * m->batch, hipMemcpyDeviceToHost, stream);
+  if (st == hipSuccess) st = hipStreamSynchronize(stream);
+  return st;
+}
+
+extern "C" hipError_t rtxllm_llama_clear_status(rtxllm_llama* m, hipStream_t stream) {
+  if (m == nullptr) return hipErrorInvalidValue;
+  hipError_t st = hipMemsetAsync(m->arena.arena_ptr("status"), 0, 4u * m->batch, stream);
+  if (st == hipSuccess) st = hipStreamSynchronize(stream);
+  return st;
 }

@@ -11,7 +11,7 @@
 //   Q4_K/Q5_K:  S_sub * (s_x * sum(q * X)) - M_sub * sum(x_hat)
 //   IQ2_S/3_S:  scale_sub * s_x * sum(+-grid * X)
 // with the integer sums from v_dot4_i32_i8 on int8 weight codes and the three
-// int8 activation digits (xq.h). Per-row partial sums of a tile are folded across the 64
+// int8 activation digits of the 22-bit staged x (xq.h). Per-row partial sums of a tile are folded across the 64
 // lanes by a butterfly transpose-reduce, which leaves row r of the tile in
 // lanes [r * 64/TILE, (r+1) * 64/TILE); wide rows (cols > 4096) split their
 // columns over KS waves of one workgroup and add the KS partials through LDS.
@@ -38,11 +38,18 @@ struct QTensor {
   std::uint32_t cols;
 };
 
-// Activation source: staged digits, or fp32 x staged by each wave itself.
+// Activation source: staged digits, or fp32 x staged by each wave itself
+// (read as float4 when x is 16-byte aligned, else value by value).
 struct XSrc {
   XQ xq;
   const float* x;
+  std::uint32_t x_aligned;
 };
+
+inline XSrc staged_src(const XQ& xq) { return XSrc{xq, nullptr, 1u}; }
+inline XSrc self_src(const float* x) {
+  return XSrc{XQ{}, x, (reinterpret_cast<std::uintptr_t>(x) % 16u) == 0u ? 1u : 0u};
+}
 
 
 // Weight streams are read through buffer resources: the row's byte offset is a
@@ -440,22 +447,24 @@ __device__ __forceinline__ IqLaneScale iq_lane_scale(std::uint32_t k, const XG& 
 template <int FMT>
 __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, const XG& x1, const IqLaneScale& ls,
                                              const IqWords& q) {
-  int ah[2], al[2];
+  int ah[2], am[2], al[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const XG& xg = s ? x1 : x0;
     ah[s] = sdot4_0(q.w[4 * s], xg.h[0]);
+    am[s] = sdot4_0(q.w[4 * s], xg.m[0]);
     al[s] = sdot4_0(q.w[4 * s], xg.l[0]);
 #pragma unroll
     for (int o = 1; o < 4; ++o) {
       const int w = static_cast<int>(q.w[4 * s + o]);
       ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o]), ah[s], false);
+      am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o]), am[s], false);
       al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
     }
   }
   const float d = h2f(r.c[0]);
-  const float D0 = static_cast<float>(dot_digits(ah[0], al[0]));
-  const float D1 = static_cast<float>(dot_digits(ah[1], al[1]));
+  const float D0 = static_cast<float>(dot_digits(ah[0], am[0], al[0]));
+  const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   if constexpr (fmt_is_iq2s(FMT)) {
     // d * (0.5 + n) / 4 * s = d * (n * s / 4 + s / 8)
     const float f0 = __builtin_fmaf(static_cast<float>(r.c[2] & 15u), ls.a0, ls.b0);
@@ -712,8 +721,13 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     std::uint32_t g0, g1;
     unit_groups<FMT>(ub[i], uk[i], g0, g1);
     if constexpr (SELF) {
-      xg_stage(xs.x, nullptr, g0, x0[i]);
-      xg_stage(xs.x, nullptr, g1, x1[i]);
+      if (xs.x_aligned != 0u) {
+        xg_stage<true>(xs.x, nullptr, g0, x0[i]);
+        xg_stage<true>(xs.x, nullptr, g1, x1[i]);
+      } else {
+        xg_stage<false>(xs.x, nullptr, g0, x0[i]);
+        xg_stage<false>(xs.x, nullptr, g1, x1[i]);
+      }
     } else {
       xg_load(xs.xq, g0, x0[i]);
       xg_load(xs.xq, g1, x1[i]);

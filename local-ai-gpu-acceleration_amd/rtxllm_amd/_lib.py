@@ -13,6 +13,8 @@ from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG_ROOT / "build" / "librtxllm.so"
+# The bench's measurement helper (a plain streaming read), not part of the library.
+PROBE_LIB_PATH = PKG_ROOT / "build" / "librtxllm_probe.so"
 
 _P = c_void_p  # device or host pointer
 _U = c_uint32
@@ -52,7 +54,14 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
     "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_memory": [_P, _P, _P, _P],
-    "rtxllm_stream_read": [_P, c_size_t, _P, _U, _S],
+    "rtxllm_llama_status": [_P, _P, _S],
+    "rtxllm_llama_clear_status": [_P, _S],
+    "rtxllm_rmsnorm_w": [_P, _P, _U, _U, c_float, _P, _S],
+    "rtxllm_rope_theta": [_P, _U, _U, c_float, _P, _U, _S],
+    "rtxllm_silu_mul": [_P, _P, c_size_t, _P, _S],
+    "rtxllm_embed_gather_q5k": [_P, _U, _U, _P, _U, _P, _S],
+    "rtxllm_attn_decode_gqa_f16": [_P, _P, _P, _P, _U, _U, _U, _U, _U, _P, _U, _P, _P, c_size_t, _S],
+    "rtxllm_argmax": [_P, _U, _U, _P, _S],
     "rtxllm_iq2s_units_pack": [_P, _U, _U, _P, _S],
     "rtxllm_iq3s_units_pack": [_P, _U, _U, _P, _S],
 }
@@ -82,6 +91,7 @@ _HOST_SIGS: dict[str, tuple] = {
     "rtxllm_xq_bytes": (c_size_t, [c_uint32]),
     "rtxllm_x16_bytes": (c_size_t, [c_uint32]),
     "rtxllm_matvec_batch_workspace": (c_size_t, [c_int, c_uint32, c_uint32]),
+    "rtxllm_attn_decode_workspace": (c_size_t, [c_uint32, c_uint32, c_uint32, c_uint32]),
     "rtxllm_llama_destroy": (None, [_P]),
     "rtxllm_llama_weights_changed": (None, [_P]),
     "rtxllm_llama_region": (_P, [_P, ctypes.c_char_p, _U, _P]),
@@ -119,6 +129,22 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_probe: ctypes.CDLL | None = None
+
+
+def probe_lib() -> ctypes.CDLL:
+    """Load build/librtxllm_probe.so, the bench's streaming-read helper."""
+    global _probe
+    if _probe is None:
+        if not PROBE_LIB_PATH.is_file():
+            raise RuntimeError(f"{PROBE_LIB_PATH} is missing: build it with `make -C {PKG_ROOT}`")
+        handle = ctypes.CDLL(os.fspath(PROBE_LIB_PATH))
+        handle.rtxllm_stream_read.restype = c_int
+        handle.rtxllm_stream_read.argtypes = [_P, c_size_t, _P, _U, _S]
+        _probe = handle
+    return _probe
+
+
 def exported_names() -> list[str]:
     return sorted(list(_LAUNCH_SIGS) + list(_HOST_SIGS))
 
@@ -134,4 +160,4 @@ def check(name: str, code: int) -> None:
         raise HipError(name, code)
 
 
-__all__ = ["lib", "check", "HipError", "exported_names", "LIB_PATH", "c_uint16"]
+__all__ = ["lib", "probe_lib", "check", "HipError", "exported_names", "LIB_PATH", "PROBE_LIB_PATH", "c_uint16"]

@@ -171,6 +171,15 @@ class Llama:
                                                                ctypes.byref(arena)))
         return {"required_bytes": req.value, "usable_bytes": use.value, "arena_bytes": arena.value}
 
+    def status(self, stream: int = 0) -> list[int]:
+        """Per-sequence status words (RTXLLM_LLAMA_STATUS_*), read synchronously."""
+        out = np.zeros(max(1, self.shape.batch), np.uint32)
+        check("rtxllm_llama_status", lib().rtxllm_llama_status(self.h, out.ctypes.data_as(c_void_p), stream))
+        return [int(v) for v in out]
+
+    def clear_status(self, stream: int = 0) -> None:
+        check("rtxllm_llama_clear_status", lib().rtxllm_llama_clear_status(self.h, stream))
+
     def launches_per_step(self) -> int:
         return int(lib().rtxllm_llama_launches_per_step(self.h))
 

@@ -60,8 +60,8 @@ _SIGS = {
     "orc_matvec_f64": (None, [c_int, _P, _P, _P, _U, _U, _P, c_int]),
     "orc_q4k_split": (None, [c_int, _P, c_size_t, _P, _P]),
     "orc_argmax": (_U, [_P, _U]),
-    "orc_stage_activation": (None, [_P, _P, _U, _P, _P, _P, _P]),
-    "orc_matvec_staged_f64": (None, [c_int, _P, _P, _P, _P, _P, _U, _U, _P, c_int]),
+    "orc_stage_activation": (None, [_P, _P, _U, _P, _P, _P, _P, _P]),
+    "orc_matvec_staged_f64": (None, [c_int, _P, _P, _P, _P, _P, _P, _U, _U, _P, c_int]),
     "orc_kv_side_write": (None, [_P, _U, _P, _U, _U, _U, _U]),
     "orc_rmsnorm_feedback": (None, [_P, _U, _P, _U, c_float]),
     "orc_silu_rmsnorm_feedback": (None, [_P, _U, _P, _U, c_float]),
@@ -78,6 +78,8 @@ _SIGS = {
     "orc_kv_append": (None, [POINTER(KvCache), _U, _P, _P]),
     "orc_attention_decode": (None, [POINTER(KvCache), _P, _U, _U, _P]),
     "orc_layer_forward": (None, [POINTER(LayerWeights), POINTER(LayerShape), POINTER(KvCache), _U, _P, c_int]),
+    "orc_layer_forward_given_kv": (None, [POINTER(LayerWeights), POINTER(LayerShape), POINTER(KvCache), _U, _P,
+                                          c_int]),
 }
 
 _lib = None
@@ -148,26 +150,27 @@ def iq3s_grid() -> np.ndarray:
 
 
 def stage_activation(x: np.ndarray, weight: np.ndarray | None = None):
-    """(H, L int8[cols], scale f32[cols/16], sum f32[cols/16])."""
+    """(H, M, L int8[cols], scale f32[cols/16], sum f32[cols/16])."""
     x = np.ascontiguousarray(x, np.float32)
     cols = x.size
-    h, l = (np.empty(cols, np.int8) for _ in range(2))
+    h, m, l = (np.empty(cols, np.int8) for _ in range(3))
     s = np.empty(cols // 16, np.float32)
     t = np.empty(cols // 16, np.float32)
     w = None if weight is None else np.ascontiguousarray(weight, np.float32)
-    lib().orc_stage_activation(ptr(x), ptr(w), cols, ptr(h), ptr(l), ptr(s), ptr(t))
-    return h, l, s, t
+    lib().orc_stage_activation(ptr(x), ptr(w), cols, ptr(h), ptr(m), ptr(l), ptr(s), ptr(t))
+    return h, m, l, s, t
 
 
 def stage_bytes(x: np.ndarray, weight: np.ndarray | None = None) -> np.ndarray:
-    """The staged activation in the product's one-buffer layout: H, L, scale, sum."""
-    h, l, s, t = stage_activation(x, weight)
-    return np.concatenate([h.view(np.uint8), l.view(np.uint8), s.view(np.uint8), t.view(np.uint8)])
+    """The staged activation in the product's one-buffer layout: H, M, L, scale, sum."""
+    h, m, l, s, t = stage_activation(x, weight)
+    return np.concatenate([h.view(np.uint8), m.view(np.uint8), l.view(np.uint8), s.view(np.uint8),
+                           t.view(np.uint8)])
 
 
 def matvec_staged_f64(fmt, payload, meta, x, rows, cols, threads=1, weight=None) -> np.ndarray:
-    h, l, s, _ = stage_activation(x, weight)
+    h, m, l, s, _ = stage_activation(x, weight)
     y = np.empty(rows, dtype=np.float64)
-    lib().orc_matvec_staged_f64(fmt, ptr(payload), ptr(meta), ptr(h), ptr(l), ptr(s), rows, cols, ptr(y),
+    lib().orc_matvec_staged_f64(fmt, ptr(payload), ptr(meta), ptr(h), ptr(m), ptr(l), ptr(s), rows, cols, ptr(y),
                                 threads)
     return y

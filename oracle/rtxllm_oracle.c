@@ -341,26 +341,33 @@ void orc_q4k_split(int fmt, const uint8_t* raw, size_t n_blocks, uint8_t* payloa
   }
 }
 
-void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* l, float* scale,
-                          float* sum) {
-  const float K = 32512.0f; /* 127 * 256 */
+void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* m, int8_t* l,
+                          float* scale, float* sum) {
   for (uint32_t g = 0; g < cols / 16u; ++g) {
     float v[16];
     float mx = 0.0f;
+    int nan = 0;
     for (int j = 0; j < 16; ++j) {
       v[j] = weight ? x[16u * g + j] * weight[16u * g + j] : x[16u * g + j];
       const float a = fabsf(v[j]);
-      if (a > mx) mx = a; /* NaN never compares greater: ignored, as fmaxf does */
+      if (isnan(v[j])) nan = 1;
+      else if (a > mx) mx = a;
     }
-    const float inv = mx > 0.0f ? K / mx : 0.0f;
-    scale[g] = mx / K;
+    /* s = 2^(e - 22) with mx = f 2^e, f in [0.5, 1); X = rint(v 2^(22 - e)) */
+    const int finite = !nan && mx <= FLT_MAX;
+    int e = 0;
+    if (finite && mx > 0.0f) (void)frexpf(mx, &e);
+    scale[g] = nan ? NAN : (!finite ? INFINITY : (mx > 0.0f ? ldexpf(1.0f, e - 22) : 0.0f));
     int total = 0;
     for (int j = 0; j < 16; ++j) {
-      const float r = rintf(v[j] * inv);
-      const int X = isnan(r) ? 0 : (r > K ? 32512 : (r < -K ? -32512 : (int)r));
-      const int H = (int)floor((X + 128) / 256.0);
-      h[16u * g + j] = (int8_t)H;
-      l[16u * g + j] = (int8_t)(X - 256 * H);
+      const int X = finite ? (int)rintf(ldexpf(v[j], 22 - e)) : 0; /* |X| <= 2^22 */
+      /* balanced base-256 digits: L, M in [-128, 127], X = 65536 H + 256 M + L */
+      const int L = X - 256 * (int)floor((X + 128) / 256.0);
+      const int X1 = (X - L) / 256;
+      const int M = X1 - 256 * (int)floor((X1 + 128) / 256.0);
+      h[16u * g + j] = (int8_t)((X1 - M) / 256);
+      m[16u * g + j] = (int8_t)M;
+      l[16u * g + j] = (int8_t)L;
       total += X;
     }
     sum[g] = scale[g] * (float)total;
@@ -370,7 +377,7 @@ void orc_stage_activation(const float* x, const float* weight, uint32_t cols, in
 typedef struct {
   int fmt;
   const uint8_t *payload, *meta;
-  const int8_t *h, *l;
+  const int8_t *h, *m, *l;
   const float* scale;
   uint32_t cols, r0, r1;
   double* y;
@@ -388,7 +395,7 @@ static void* st_worker(void* arg) {
       const uint8_t* mt = blk_ptr(j->meta, mb, bi);
       for (uint32_t v = 0; v < 256u; ++v) {
         const uint32_t c = b * 256u + v;
-        const double X = 256.0 * j->h[c] + j->l[c];
+        const double X = 65536.0 * j->h[c] + 256.0 * j->m[c] + j->l[c];
         acc += (double)orc_dequant_value(j->fmt, p, mt, v) * ((double)j->scale[c / 16u] * X);
       }
     }
@@ -397,15 +404,16 @@ static void* st_worker(void* arg) {
   return NULL;
 }
 
-void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* l,
-                           const float* scale, uint32_t rows, uint32_t cols, double* y, int nthreads) {
+void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h, const int8_t* m,
+                           const int8_t* l, const float* scale, uint32_t rows, uint32_t cols, double* y,
+                           int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > 64) nthreads = 64;
   if ((uint32_t)nthreads > rows) nthreads = rows ? (int)rows : 1;
   st_job jobs[64];
   pthread_t th[64];
   for (int t = 0; t < nthreads; ++t) {
-    st_job jb = {fmt, payload, meta, h, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
+    st_job jb = {fmt, payload, meta, h, m, l, scale, cols, (uint32_t)((uint64_t)rows * t / nthreads),
                  (uint32_t)((uint64_t)rows * (t + 1) / nthreads), y};
     jobs[t] = jb;
   }
@@ -608,8 +616,8 @@ void orc_attention_decode(const orc_kv_cache* kv, const float* q, uint32_t n_hea
   free(acc);
 }
 
-void orc_layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv, uint32_t pos,
-                       float* h, int nthreads) {
+static void layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv, uint32_t pos,
+                          float* h, int nthreads, int append) {
   const uint32_t H = s->hidden, qd = s->n_heads * s->head_dim, kvd = s->n_kv_heads * s->head_dim;
   float* xn = (float*)malloc(sizeof(float) * (H > s->ffn ? H : s->ffn));
   float* q = (float*)malloc(sizeof(float) * qd);
@@ -626,7 +634,7 @@ void orc_layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc
   orc_matvec_f32(w->fmt_v, w->wv, w->wv_meta, xn, kvd, H, v, nthreads);
   orc_rope(q, s->n_heads, s->head_dim, s->inv_freq, pos);
   orc_rope(k, s->n_kv_heads, s->head_dim, s->inv_freq, pos);
-  orc_kv_append(kv, pos, k, v);
+  if (append) orc_kv_append(kv, pos, k, v);
   orc_attention_decode(kv, q, s->n_heads, pos, att);
   orc_matvec_f32(w->fmt_o, w->wo, w->wo_meta, att, H, qd, o, nthreads);
   for (uint32_t i = 0; i < H; ++i) h[i] += o[i];
@@ -646,4 +654,14 @@ void orc_layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc
   free(o);
   free(g);
   free(u);
+}
+
+void orc_layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv, uint32_t pos,
+                       float* h, int nthreads) {
+  layer_forward(w, s, kv, pos, h, nthreads, 1);
+}
+
+void orc_layer_forward_given_kv(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv,
+                                uint32_t pos, float* h, int nthreads) {
+  layer_forward(w, s, kv, pos, h, nthreads, 0);
 }

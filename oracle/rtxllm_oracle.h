@@ -63,16 +63,18 @@ void orc_q4k_split(int fmt, const uint8_t* raw_blocks, size_t n_blocks, uint8_t*
                    uint8_t* meta);
 
 /* Activation staging of the product's integer-dot matvec (its own design, no
- * reference counterpart): per 16-value group, m = max|v|, s = m / K with
- * K = 127 * 256, X = clamp(rint(v * (K / m)), +-K), digits H = floor((X +
- * 128) / 256), L = X - 256 H, sum = s * sum(X). v = x * weight when weight is
+ * reference counterpart): per 16-value group, m = max|v| (NaN ignored) = f 2^e
+ * with f in [0.5, 1), s = 2^(e - 22), X = rint(v 2^(22 - e)) (|X| <= 2^22),
+ * digits X = 65536 H + 256 M + L with M, L in [-128, 127], sum = s * sum(X).
+ * A group holding a NaN gets s = NaN, one with an infinite maximum s = inf,
+ * both zero digits; an all-zero group s = 0. v = x * weight when weight is
  * non-null. */
-void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* l,
+void orc_stage_activation(const float* x, const float* weight, uint32_t cols, int8_t* h, int8_t* m, int8_t* l,
                           float* scale, float* sum);
 /* y = W x_hat with x_hat = s * X (the staged activation), accumulated in double. */
 void orc_matvec_staged_f64(int fmt, const uint8_t* payload, const uint8_t* meta, const int8_t* h,
-                           const int8_t* l, const float* scale, uint32_t rows, uint32_t cols, double* y,
-                           int nthreads);
+                           const int8_t* m, const int8_t* l, const float* scale, uint32_t rows, uint32_t cols,
+                           double* y, int nthreads);
 
 /* Greedy token: lowest index among the maxima; start (-FLT_MAX, 0). */
 uint32_t orc_argmax(const float* y, uint32_t n);
@@ -134,6 +136,11 @@ typedef struct {
 
 void orc_layer_forward(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv,
                        uint32_t pos, float* h, int nthreads);
+/* The same layer with the cache taken as given: the K / V of position pos are
+ * already in it (no append), so a caller can run the layer on exactly the
+ * cache state another implementation wrote (its own fp16 rounding of k and v). */
+void orc_layer_forward_given_kv(const orc_layer_weights* w, const orc_layer_shape* s, orc_kv_cache* kv,
+                                uint32_t pos, float* h, int nthreads);
 
 #ifdef __cplusplus
 }

@@ -74,10 +74,12 @@ class HostModel:
             self.lm_meta = None
         self.out_norm = m.download("out_norm", np.float32)
 
-    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True, layers=None, seq: int = 0):
+    def run(self, orc, h: np.ndarray, pos: int, threads: int = 8, head: bool = True, layers=None, seq: int = 0,
+            given_kv: bool = False):
         """Layers (all of this model's, or the given subset) in place on h
         (float32) for sequence `seq` (its block-table row and KV pages);
-        returns (h, logits or None)."""
+        returns (h, logits or None). given_kv: the host caches already hold the
+        K / V of `pos` (no append; orc_layer_forward_given_kv)."""
         s, f, P = self.m.shape, self.m.formats, orc.ptr
         lib = orc.lib()
         inv_freq = np.empty(HEAD_DIM // 2, np.float32)
@@ -94,13 +96,29 @@ class HostModel:
             pps = s.max_ctx // s.page_size
             table = np.ascontiguousarray(d["block_table"][seq * pps:(seq + 1) * pps])
             kv = orc.KvCache(P(d["k_cache"]), P(d["v_cache"]), P(table), s.page_size, s.n_kv_heads, HEAD_DIM)
-            lib.orc_layer_forward(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(kv), pos, P(h), threads)
+            fwd = lib.orc_layer_forward_given_kv if given_kv else lib.orc_layer_forward
+            fwd(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(kv), pos, P(h), threads)
         if not head:
             return h, None
         xn = np.empty_like(h)
         lib.orc_rmsnorm_weighted(P(h), P(self.out_norm), s.hidden, s.rms_eps, P(xn))
         logits = orc.matvec_f32(f["fmt_lm_head"], self.lm_head, self.lm_meta, xn, s.vocab, s.hidden, threads)
         return h, logits
+
+    def kv_of(self, orc, h: np.ndarray, pos: int, layer: int) -> tuple[np.ndarray, np.ndarray]:
+        """The oracle's fp32 k (rotated) and v of layer `layer` for input h at pos."""
+        s, f, P = self.m.shape, self.m.formats, orc.ptr
+        lib = orc.lib()
+        d = self.L[layer]
+        xn = np.empty(s.hidden, np.float32)
+        hh = np.ascontiguousarray(h, np.float32)
+        lib.orc_rmsnorm_weighted(P(hh), P(d["attn_norm"]), s.hidden, s.rms_eps, P(xn))
+        k = orc.matvec_f32(f["fmt_qkv"], d["wk"], d["wk_meta"], xn, self.kv_rows, s.hidden, 8)
+        v = orc.matvec_f32(f["fmt_qkv"], d["wv"], d["wv_meta"], xn, self.kv_rows, s.hidden, 8)
+        inv_freq = np.empty(HEAD_DIM // 2, np.float32)
+        lib.orc_rope_inv_freq(HEAD_DIM, s.rope_theta, P(inv_freq))
+        lib.orc_rope(P(k), s.n_kv_heads, HEAD_DIM, P(inv_freq), pos)
+        return k, v
 
     def embed_row(self, orc, token: int) -> np.ndarray:
         out = np.empty(self.m.shape.hidden, np.float32)

@@ -19,7 +19,8 @@ def declared_functions() -> list[str]:
     names = []
     for hdr in sorted((REPO / "include" / "rtxllm").glob("*.h")):
         text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
-        names += re.findall(r"^\s*(?:hipError_t|int|uint32_t|void)\s+(rtxllm_\w+)\s*\(", text, flags=re.M)
+        names += re.findall(r"^\s*(?:hipError_t|int|uint32_t|size_t|void\s*\*|void)\s*(rtxllm_\w+)\s*\(", text,
+                            flags=re.M)
     return names
 
 
@@ -28,6 +29,15 @@ def test_library_exports_every_declared_symbol(rlib):
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(rlib, n)]
     assert not missing, missing
+
+
+def test_measurement_probe_is_not_in_the_library(rlib):
+    """The streaming-read probe lives in the bench's own helper library."""
+    from rtxllm_amd import _lib
+
+    assert not hasattr(rlib, "rtxllm_stream_read")
+    assert "rtxllm_stream_read" not in declared_functions()
+    assert hasattr(_lib.probe_lib(), "rtxllm_stream_read")
 
 
 def test_binding_covers_declared_symbols():

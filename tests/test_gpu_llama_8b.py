@@ -110,3 +110,28 @@ def test_8b_decode_step_each_stage_matches_oracle(orc, model8b):
         assert tok == int(np.argmax(logits_ref))
     assert int(m.download("pos", np.uint32)[0]) == pos + 1
     print(f"worst per-layer relative error {worst:.2e}")
+
+
+def test_8b_graph_replay_bit_identical_to_eager(model8b):
+    """The captured 32-layer step (195 launches, the down epilogue's fused
+    next-layer staging at every layer boundary) equals the eager step bit for
+    bit, replay after replay."""
+    m = model8b
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    token, pos = 777, LLAMA_8B.max_ctx - 1
+    m.set_token_pos(token, pos)
+    m.step(sp)
+    torch.cuda.synchronize()
+    eager_logits = m.download("logits", np.float32)
+    eager_h = m.download("h", np.float32)
+    eager_tok = int(m.download("token", np.uint32)[0])
+    assert int(m.download("pos", np.uint32)[0]) == pos + 1
+    m.graph_capture(sp)
+    for _ in range(3):  # a step at the same position rewrites the same KV slot
+        m.set_token_pos(token, pos)
+        m.graph_replay(sp)
+        torch.cuda.synchronize()
+        assert np.array_equal(m.download("logits", np.float32).view(np.uint32), eager_logits.view(np.uint32))
+        assert np.array_equal(m.download("h", np.float32).view(np.uint32), eager_h.view(np.uint32))
+        assert int(m.download("token", np.uint32)[0]) == eager_tok

@@ -65,7 +65,22 @@ def model():
 
 
 def test_batch_step_matches_oracle_per_sequence(orc, model):
-    m, s = model, SMALL_B
+    check_step(orc, model, SMALL_B)
+
+
+def test_batch_step_wide_ffn_panel_groups(orc):
+    """ffn 4608 > 4096 columns: the down projection splits into two panel
+    groups, whose partial sums the residual staging adds per sequence."""
+    s = Shape(hidden=512, n_heads=4, n_kv_heads=2, ffn=4608, vocab=1000, n_layers=2, max_ctx=256, page_size=16,
+              batch=B)
+    m = build(s, SEED + 7)
+    try:
+        check_step(orc, m, s)
+    finally:
+        m.close()
+
+
+def check_step(orc, m, s):
     m.set_token_pos(TOKENS, POSITIONS)
     ref = HostModel(m, range(s.n_layers))
     k_before = {l: ref.L[l]["k_cache"].copy() for l in range(s.n_layers)}

@@ -230,7 +230,7 @@ def tiny_layer(orc, seed, zero_o=False, zero_down=False):
     return dict(H=H, nh=nh, nkv=nkv, hd=hd, ff=ff, f=(fq, fo, fgu, fdn), w=(wq, wk, wv, wo, wg, wu, wd), an=an, fn=fn)
 
 
-def run_layer(orc, L, h, pos, kvc):
+def run_layer(orc, L, h, pos, kvc, given_kv=False):
     P = orc.ptr
     wq, wk, wv, wo, wg, wu, wd = L["w"]
     fq, fo, fgu, fdn = L["f"]
@@ -241,8 +241,26 @@ def run_layer(orc, L, h, pos, kvc):
     orc.lib().orc_rope_inv_freq(L["hd"], 500000.0, P(inv))
     shape = orc.LayerShape(L["H"], L["nh"], L["nkv"], L["hd"], L["ff"], 1e-6, P(inv))
     out = h.copy()
-    orc.lib().orc_layer_forward(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(kvc), pos, P(out), 1)
+    fwd = orc.lib().orc_layer_forward_given_kv if given_kv else orc.lib().orc_layer_forward
+    fwd(ctypes.byref(w), ctypes.byref(shape), ctypes.byref(kvc), pos, P(out), 1)
     return out
+
+
+def test_layer_given_kv_equals_layer_on_the_same_cache(orc):
+    """orc_layer_forward_given_kv on the cache state orc_layer_forward left
+    (its own K / V of pos appended) gives the same h bit for bit; on a cache
+    whose slot holds other values it differs (the slot is really read)."""
+    L = tiny_layer(orc, 0x5EED2200)
+    kvc, kpages, vpages, _ = make_cache(orc, 2, L["nkv"], 16, L["hd"])
+    for p in range(5):
+        append(orc, kvc, p, packs.normal_f32(0x5EED2300 + p, L["nkv"] * L["hd"]),
+               packs.normal_f32(0x5EED2400 + p, L["nkv"] * L["hd"]))
+    h = packs.normal_f32(0x5EED2500, L["H"])
+    out = run_layer(orc, L, h, 5, kvc)  # appends its K / V of position 5
+    again = run_layer(orc, L, h, 5, kvc, given_kv=True)
+    assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+    append(orc, kvc, 5, np.zeros(L["nkv"] * L["hd"], np.float32), np.zeros(L["nkv"] * L["hd"], np.float32))
+    assert not np.array_equal(run_layer(orc, L, h, 5, kvc, given_kv=True), out)
 
 
 def test_layer_zero_branches_are_identity(orc):
