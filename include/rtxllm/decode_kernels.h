@@ -263,6 +263,21 @@ size_t rtxllm_matvec_batch_workspace(int format, uint32_t rows, uint32_t cols);
 hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
                                float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same without a workspace argument, for callers that cannot allocate
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference. The panel groups' partial sums
+ * go to a scratch array of RTXLLM_NOALLOC_SCRATCH_BYTES that the library
+ * holds on every GPU it runs on until the process ends; its address is looked
+ * up on the first call on each device. Calls whose 4 * batch * rows * panel
+ * groups bytes exceed it are refused with hipErrorInvalidValue (matrices of
+ * at most 4096 columns have one panel group and need none). Every call on a
+ * GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams, other host threads) race; calls in one stream are ordered. Nothing
+ * is allocated, freed or cleared: each call writes every partial sum it reads. */
+#define RTXLLM_NOALLOC_SCRATCH_BYTES (8u << 20)
+hipError_t rtxllm_matvec_batch_noalloc(int format, const uint8_t* payload, const uint8_t* meta, const void* x16,
+                                       float* y /* [batch][rows] */, uint32_t rows, uint32_t cols, uint32_t batch,
+                                       hipStream_t stream);
 /* The same from the fp32 activation x [batch][cols] (16-byte aligned): every
  * wave stages its own 512 columns with the rtxllm_stage_batch rule, so the
  * result equals rtxllm_stage_batch + rtxllm_matvec_batch bit for bit without

@@ -4,6 +4,7 @@
 // qkv (RoPE + KV append), gate/up (SiLU-gate) and LM-head (logits + argmax
 // keys) projections.
 #include <algorithm>
+#include <mutex>
 
 #include "dequant.cuh"
 #include "internal.h"
@@ -11,6 +12,7 @@
 #include "layer_common.cuh"
 #include "mm.cuh"
 #include "mv_launch.cuh"
+#include "rtxllm/decode_kernels.h"
 
 namespace rtxllm {
 namespace {
@@ -429,6 +431,55 @@ extern "C" hipError_t rtxllm_matvec_batch(int format, const uint8_t* payload, co
                                           float* y, uint32_t rows, uint32_t cols, uint32_t batch, void* workspace,
                                           size_t workspace_bytes, hipStream_t stream) {
   return matvec_batch(format, payload, meta, x16, false, y, rows, cols, batch, workspace, workspace_bytes, stream);
+}
+
+// ---- allocation-free batched matvec ------------------------------------------
+// The panel groups' partial sums of rtxllm_matvec_batch_noalloc go to this
+// file-scope array instead of a caller's workspace: each GPU the library runs on
+// holds its own copy until the process ends. Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol); it
+// passes the device address hipGetSymbolAddress returns for the current
+// device, looked up on the entry point's first call on that device.
+static __device__ __align__(256) std::uint8_t scratch[RTXLLM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+hipError_t scratch_address(void** out) {
+  int dev = 0;
+  hipError_t st = hipGetDevice(&dev);
+  if (st != hipSuccess) return st;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st != hipSuccess) return st;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_matvec_batch_noalloc(int format, const uint8_t* payload, const uint8_t* meta,
+                                                  const void* x16, float* y, uint32_t rows, uint32_t cols,
+                                                  uint32_t batch, hipStream_t stream) {
+  if (batch == 0u || batch > kBatchMax) return hipErrorInvalidValue;
+  const std::uint32_t groups = mm_panel_groups(format, rows, cols);
+  if (groups == 0u) return hipErrorInvalidValue;
+  const std::size_t need = groups > 1u ? 4u * static_cast<std::size_t>(batch) * rows * groups : 0u;
+  if (need > RTXLLM_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;  // beyond the scratch array
+  void* ws = nullptr;
+  const hipError_t st = scratch_address(&ws);
+  if (st != hipSuccess) return st;
+  return matvec_batch(format, payload, meta, x16, false, y, rows, cols, batch, ws, RTXLLM_NOALLOC_SCRATCH_BYTES,
+                      stream);
 }
 
 extern "C" hipError_t rtxllm_matvec_batch_f32(int format, const uint8_t* payload, const uint8_t* meta, const float* x,
