@@ -60,6 +60,13 @@ def parse() -> argparse.Namespace:
                     help="run the batch-8 matvec stages of one layer (the matrix-core counter workload)")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
                     help="matrix-core FLOP and rate per batch matvec kernel from the counter and trace runs")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="per-kernel launch statistics of a rocprofv3 --kernel-trace run as a markdown table, "
+                         "with the kernels both decode paths launch split by grid size")
+    ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR",
+                    help="instruction accounting per decode stage kernel from rocprofv3 --pmc runs of "
+                         "--traffic-probe (SQ_* counters, any split over passes), with the VALU issue floor "
+                         "against the time budget at 70%% of the HBM peak")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -404,6 +411,129 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+def _short_kernel(name: str) -> str:
+    """Readable kernel name: namespaces and parameter lists dropped. Names the
+    profiler left mangled (those with _Float16 parameters) are read as
+    _ZN <len><id>... [I Li<n>E... E]: the last identifier plus its integer
+    template arguments."""
+    import re
+
+    if name.startswith("_ZN"):
+        i, ident = 3, ""
+        while i < len(name) and name[i].isdigit():
+            m = re.match(r"\d+", name[i:])
+            n = int(m.group(0))
+            i += len(m.group(0))
+            ident = name[i:i + n]
+            i += n
+        targs = re.match(r"I((?:Li\d+E)+)E", name[i:])
+        if targs:
+            ident += "<" + ", ".join(re.findall(r"Li(\d+)E", targs.group(1))) + ">"
+        return ident
+    n = re.sub(r"rtxllm::\(anonymous namespace\)::|rtxllm::", "", name).replace("void ", "")
+    return n.split("(")[0] if "(" in n else n
+
+
+def trace_summary(trace_dir: str) -> str:
+    """Per-kernel count / mean / min / max launch time (us) and share of GPU time
+    from the kernel trace of one run. The batch-1 and batch-8 steps launch the
+    same attention and argmax kernels; their launches are told apart by the grid
+    dimension that counts sequences (attention partials: z, combine: y,
+    argmax finalize: x / 256)."""
+    import csv
+    import glob
+    import statistics
+
+    rows: dict = {}
+    for f in glob.glob(str(Path(trace_dir) / "**" / "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            name = _short_kernel(r["Kernel_Name"])
+            gx, gy, gz = int(r["Grid_Size_X"]), int(r["Grid_Size_Y"]), int(r["Grid_Size_Z"])
+            seqs = None
+            if name.startswith("attn_partial"):
+                seqs = gz
+            elif name.startswith("attn_combine"):
+                seqs = gy
+            elif name.startswith("argmax_finalize"):
+                seqs = max(1, gx // 256)
+            if seqs is not None:
+                name += f" (batch {seqs})"
+            rows.setdefault(name, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    if not rows:
+        raise SystemExit(f"no kernel trace under {trace_dir}")
+    total = sum(sum(v) for v in rows.values())
+    lines = ["| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---:|---:|---:|---:|---:|"]
+    for k, v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        if sum(v) / total < 0.002:
+            continue
+        lines.append(f"| `{k}` | {len(v)} | {statistics.mean(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                     f"{100 * sum(v) / total:.2f} |")
+    return "\n".join(lines) + "\n"
+
+
+ENGINE_CLOCK_GHZ = 2.4     # MI355X peak engine clock
+SIMDS = 256 * 4            # 256 CUs x 4 SIMDs
+VALU_CYCLES_PER_OP = 4     # a wave64 VALU instruction on a 16-lane SIMD
+STAGE_UNITS = {  # 32-value weight units per launch at the 8B shapes (rows x cols / 32)
+    "qkv": 6144 * 4096 // 32, "o": 4096 * 4096 // 32, "gate_up": 28672 * 4096 // 32,
+    "down": 4096 * 14336 // 32, "lm_head": 128256 * 4096 // 32,
+}
+STAGE_BYTES = {"qkv": 10813440, "attention": 16672768, "o": 7208960, "gate_up": 37617664, "down": 33030144,
+               "lm_head": 361168896}
+
+
+def counter_summary(pmc_dirs) -> str:
+    """Per decode-stage kernel, the mean per dispatch of every SQ counter found
+    in the given --pmc runs of --traffic-probe, and derived figures:
+    instructions per wave; per 64 weight units (one unit per lane: a wave's
+    pass over 64 units), which is the cost per pass of the batch-1 matvecs;
+    wait / VALU-active shares of wave cycles; LDS bank conflicts per LDS-active
+    cycle. The VALU floor is the time the SIMDs need to issue the launch's
+    VALU instructions (4 cycles each on 1024 SIMDs at 2.4 GHz); the budget is
+    the time of the launch's algorithmic bytes at 70 % of 8 TB/s."""
+    import csv
+    import glob
+
+    vals: dict = {}
+    for d in pmc_dirs:
+        for f in glob.glob(str(Path(d) / "**" / "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                for st, key in STAGE_KERNELS.items():
+                    if key in r["Kernel_Name"]:
+                        vals.setdefault(st, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit("no decode stage kernel in the counter runs")
+    lines = []
+    for st in STAGE_KERNELS:
+        if st not in vals:
+            continue
+        c = {k: sum(v) / len(v) for k, v in vals[st].items()}
+        parts = [st] + [f"{k} {c[k]:.0f}" for k in sorted(c)]
+        waves = c.get("SQ_WAVES")
+        if waves:
+            for k in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD", "SQ_INSTS_SMEM"):
+                if k in c:
+                    parts.append(f"{k.replace('SQ_INSTS_', '').lower()}_per_wave {c[k] / waves:.1f}")
+        if st in STAGE_UNITS:
+            passes = STAGE_UNITS[st] / 64.0
+            for k in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD"):
+                if k in c:
+                    parts.append(f"{k.replace('SQ_INSTS_', '').lower()}_per_64_units {c[k] / passes:.1f}")
+        if "SQ_WAVE_CYCLES" in c and c["SQ_WAVE_CYCLES"] > 0:
+            for k in ("SQ_WAIT_ANY", "SQ_ACTIVE_INST_VALU", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS"):
+                if k in c:
+                    parts.append(f"{k.replace('SQ_', '').lower()}_share {c[k] / c['SQ_WAVE_CYCLES']:.3f}")
+        if c.get("SQ_ACTIVE_INST_LDS"):
+            if "SQ_LDS_BANK_CONFLICT" in c:
+                parts.append(f"lds_conflict_per_active {c['SQ_LDS_BANK_CONFLICT'] / c['SQ_ACTIVE_INST_LDS']:.3f}")
+        if "SQ_INSTS_VALU" in c:
+            floor = c["SQ_INSTS_VALU"] * VALU_CYCLES_PER_OP / (ENGINE_CLOCK_GHZ * 1e3 * SIMDS)
+            budget = STAGE_BYTES[st] / (0.7 * HBM_PEAK_GBS * 1e3)
+            parts.append(f"valu_floor_us {floor:.2f} budget_us_at_70pct {budget:.2f}")
+        lines.append(" ".join(parts))
+    return "\n".join(lines) + "\n"
+
+
 def traffic_of(stage: str):
     """HBM bytes per launch of a stage from the committed counter summary, or None."""
     try:
@@ -672,6 +802,12 @@ def main() -> int:
         return 0
     if args.mfma_summary:
         sys.stdout.write(mfma_summary(*args.mfma_summary))
+        return 0
+    if args.counter_summary:
+        sys.stdout.write(counter_summary(args.counter_summary))
+        return 0
+    if args.trace_summary:
+        sys.stdout.write(trace_summary(args.trace_summary))
         return 0
     import torch
 
