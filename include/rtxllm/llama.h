@@ -118,6 +118,14 @@ hipError_t rtxllm_llama_synth_weights(rtxllm_llama* m, uint64_t seed, hipStream_
 hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_manifest, const char* iq_manifest,
                                    const char* payload_root, char* err, size_t err_len);
 
+/* rtxllm_llama_load_packs over any number of manifests (count entries), each
+ * read by the loader its "path" field names: the reference producers write one
+ * manifest per producer (q4k_resident_pack, iq_resident_pack,
+ * q5k_resident_pack), as does rtxllm_gguf_pack (rtxllm/pack_producer.h). A
+ * tensor in two manifests is refused; the rest as rtxllm_llama_load_packs. */
+hipError_t rtxllm_llama_load_pack_set(rtxllm_llama* m, const char* const* manifests, uint32_t count,
+                                      const char* payload_root, char* err, size_t err_len);
+
 /* The admission check made at create: bytes the model needs (weights, KV,
  * workspace, graph), the device bytes it was admitted against, and the arena
  * size. */

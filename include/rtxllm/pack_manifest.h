@@ -136,6 +136,13 @@ std::vector<std::uint8_t> load_binary_file(const std::filesystem::path& path, st
 // "split-half", "split-compact", "split-native"), or -1.
 int q4k_policy_format(const std::string& policy);
 
+// Which loader reads a manifest: its "path" field names the producer
+// ("q4k_resident_pack"; "iq_resident_pack" or "q5k_resident_pack" for raw
+// blocks); without one, Q4_K records carry "metadata_path" and raw-block
+// records "type". Throws when neither tells.
+enum class PackManifestKind { Q4K, RawBlocks };
+PackManifestKind pack_manifest_kind(const std::filesystem::path& path);
+
 }  // namespace rtxllm
 
 #endif

@@ -8,6 +8,7 @@
 // 4825-4836), for a real Llama layer instead of its synthetic stages.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -418,16 +419,26 @@ void verify(const std::vector<std::uint8_t>& bytes, std::uint64_t checksum, cons
   if (rtxllm::byte_checksum(bytes) != checksum) throw std::runtime_error("checksum mismatch: " + what);
 }
 
+struct ManifestRef {
+  rtxllm::PackManifestKind kind;
+  std::string path;
+};
+
 // GGUF tensors of the manifests, by name. A Q4_K tensor is read in the layout
 // the runner's config wants for it (`want` maps a tensor name to its format):
 // a split layout from its payload + metadata files (the manifest's policy
-// must be that layout), the raw blocks from blocks_path.
-std::map<std::string, PackTensor> read_packs(const char* q4k_manifest, const char* iq_manifest,
+// must be that layout), the raw blocks from blocks_path. A tensor named in
+// two manifests is refused.
+std::map<std::string, PackTensor> read_packs(const std::vector<ManifestRef>& manifests,
                                              const std::filesystem::path& root,
                                              const std::map<std::string, int>& want) {
   std::map<std::string, PackTensor> out;
-  if (q4k_manifest != nullptr && *q4k_manifest != '\0') {
-    const rtxllm::Q4KManifest man = rtxllm::load_q4k_manifest(q4k_manifest);
+  auto keep = [&](const std::string& name, PackTensor&& pt) {
+    if (!out.emplace(name, std::move(pt)).second) throw std::runtime_error("tensor in two manifests: " + name);
+  };
+  for (const ManifestRef& ref : manifests) {
+    if (ref.kind != rtxllm::PackManifestKind::Q4K) continue;
+    const rtxllm::Q4KManifest man = rtxllm::load_q4k_manifest(ref.path);
     for (const auto& t : man.tensors) {
       const auto w = want.find(t.name);
       if (w == want.end()) continue;
@@ -450,11 +461,12 @@ std::map<std::string, PackTensor> read_packs(const char* q4k_manifest, const cha
             pt.meta.size() != blocks * rtxllm_format_meta_bytes(pt.fmt))
           throw std::runtime_error("Q4_K pack stream sizes disagree with the shape: " + t.name);
       }
-      out[t.name] = std::move(pt);
+      keep(t.name, std::move(pt));
     }
   }
-  if (iq_manifest != nullptr && *iq_manifest != '\0') {
-    const rtxllm::IQManifest man = rtxllm::load_iq_manifest(iq_manifest);
+  for (const ManifestRef& ref : manifests) {
+    if (ref.kind != rtxllm::PackManifestKind::RawBlocks) continue;
+    const rtxllm::IQManifest man = rtxllm::load_iq_manifest(ref.path);
     static const std::map<std::string, int> kType = {
         {"IQ2_S", RTXLLM_FMT_IQ2S}, {"IQ3_S", RTXLLM_FMT_IQ3S}, {"Q5_K", RTXLLM_FMT_Q5K}};
     for (const auto& t : man.tensors) {
@@ -469,16 +481,45 @@ std::map<std::string, PackTensor> read_packs(const char* q4k_manifest, const cha
         throw std::runtime_error("raw-block pack geometry disagrees with its dimensions: " + t.name);
       pt.payload = rtxllm::load_binary_file(under(root, t.payload_path), t.payload_bytes, "raw blocks");
       verify(pt.payload, t.payload_checksum, t.name);
-      out[t.name] = std::move(pt);
+      keep(t.name, std::move(pt));
     }
   }
   return out;
 }
 
+hipError_t load_manifests(rtxllm_llama* m, const std::vector<ManifestRef>& manifests, const char* payload_root,
+                          char* err, size_t err_len);
+
 }  // namespace
 
 extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_manifest, const char* iq_manifest,
                                               const char* payload_root, char* err, size_t err_len) {
+  std::vector<ManifestRef> refs;
+  if (q4k_manifest != nullptr && *q4k_manifest != '\0') refs.push_back({rtxllm::PackManifestKind::Q4K, q4k_manifest});
+  if (iq_manifest != nullptr && *iq_manifest != '\0') refs.push_back({rtxllm::PackManifestKind::RawBlocks, iq_manifest});
+  return load_manifests(m, refs, payload_root, err, err_len);
+}
+
+extern "C" hipError_t rtxllm_llama_load_pack_set(rtxllm_llama* m, const char* const* manifests, uint32_t count,
+                                                 const char* payload_root, char* err, size_t err_len) {
+  std::vector<ManifestRef> refs;
+  try {
+    if (manifests == nullptr && count != 0) throw std::runtime_error("manifests is null");
+    for (uint32_t i = 0; i < count; ++i) {
+      if (manifests[i] == nullptr || *manifests[i] == '\0') throw std::runtime_error("empty manifest path");
+      refs.push_back({rtxllm::pack_manifest_kind(manifests[i]), manifests[i]});
+    }
+  } catch (const std::exception& e) {
+    if (err != nullptr && err_len > 0) std::snprintf(err, err_len, "%s", e.what());
+    return hipErrorInvalidValue;
+  }
+  return load_manifests(m, refs, payload_root, err, err_len);
+}
+
+namespace {
+
+hipError_t load_manifests(rtxllm_llama* m, const std::vector<ManifestRef>& manifests, const char* payload_root,
+                          char* err, size_t err_len) {
   auto report = [&](const std::string& what) {
     if (err != nullptr && err_len > 0) {
       const std::size_t n = std::min(what.size(), err_len - 1u);
@@ -510,7 +551,7 @@ extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_m
   std::map<std::string, int> want;
   for (const auto& kv : need) want[kv.first] = kv.second.fmt;
   try {
-    const auto packs = read_packs(q4k_manifest, iq_manifest, payload_root != nullptr ? payload_root : "", want);
+    const auto packs = read_packs(manifests, payload_root != nullptr ? payload_root : "", want);
     auto get = [&](const std::string& name) -> const PackTensor& {
       const auto it = packs.find(name);
       if (it == packs.end()) throw std::runtime_error("tensor missing from the packs: " + name);
@@ -585,6 +626,8 @@ extern "C" hipError_t rtxllm_llama_load_packs(rtxllm_llama* m, const char* q4k_m
   report("");
   return hipSuccess;
 }
+
+}  // namespace
 
 extern "C" hipError_t rtxllm_llama_memory(const rtxllm_llama* m, size_t* required_bytes, size_t* usable_bytes,
                                           size_t* arena_bytes) {

@@ -3,6 +3,8 @@
 // validation rules to it (see include/rtxllm/pack_manifest.h).
 #include "rtxllm/pack_manifest.h"
 
+#include "json_value.h"
+
 #include <algorithm>
 #include <cstring>
 #include <fstream>
@@ -18,210 +20,12 @@ namespace {
 
 [[noreturn]] void fail(const std::string& what) { throw std::runtime_error(what); }
 
-// ---- JSON value tree --------------------------------------------------------------
-
-struct Json {
-  enum Kind { Null, Bool, Number, String, Array, Object } kind = Null;
-  bool b = false;
-  std::string text;  // String: the value; Number: its literal
-  std::vector<Json> items;
-  std::vector<std::pair<std::string, Json>> members;
-
-  const Json* find(std::string_view key) const {
-    if (kind != Object) return nullptr;
-    for (const auto& m : members)
-      if (m.first == key) return &m.second;
-    return nullptr;
-  }
-};
-
-class Reader {
- public:
-  explicit Reader(std::string_view s) : s_(s) {}
-  Json document() {
-    Json v = value(0);
-    ws();
-    if (i_ != s_.size()) error("trailing characters");
-    return v;
-  }
-
- private:
-  std::string_view s_;
-  std::size_t i_ = 0;
-  static constexpr int kMaxDepth = 256;
-
-  [[noreturn]] void error(const char* what) const {
-    fail(std::string("manifest JSON: ") + what + " at byte " + std::to_string(i_));
-  }
-  void ws() {
-    while (i_ < s_.size() && (s_[i_] == ' ' || s_[i_] == '\t' || s_[i_] == '\n' || s_[i_] == '\r')) ++i_;
-  }
-  bool take(char c) {
-    ws();
-    if (i_ < s_.size() && s_[i_] == c) {
-      ++i_;
-      return true;
-    }
-    return false;
-  }
-  void expect(char c) {
-    if (!take(c)) error("unexpected character");
-  }
-  bool literal(std::string_view word) {
-    if (s_.compare(i_, word.size(), word) != 0) return false;
-    i_ += word.size();
-    return true;
-  }
-  static void utf8(std::string& out, std::uint32_t cp) {
-    if (cp < 0x80) {
-      out += static_cast<char>(cp);
-    } else if (cp < 0x800) {
-      out += static_cast<char>(0xC0 | (cp >> 6));
-      out += static_cast<char>(0x80 | (cp & 0x3F));
-    } else if (cp < 0x10000) {
-      out += static_cast<char>(0xE0 | (cp >> 12));
-      out += static_cast<char>(0x80 | ((cp >> 6) & 0x3F));
-      out += static_cast<char>(0x80 | (cp & 0x3F));
-    } else {
-      out += static_cast<char>(0xF0 | (cp >> 18));
-      out += static_cast<char>(0x80 | ((cp >> 12) & 0x3F));
-      out += static_cast<char>(0x80 | ((cp >> 6) & 0x3F));
-      out += static_cast<char>(0x80 | (cp & 0x3F));
-    }
-  }
-  std::uint32_t hex4() {
-    if (i_ + 4 > s_.size()) error("short \\u escape");
-    std::uint32_t v = 0;
-    for (int k = 0; k < 4; ++k) {
-      const char c = s_[i_++];
-      v <<= 4;
-      if (c >= '0' && c <= '9') v |= static_cast<std::uint32_t>(c - '0');
-      else if (c >= 'a' && c <= 'f') v |= static_cast<std::uint32_t>(c - 'a' + 10);
-      else if (c >= 'A' && c <= 'F') v |= static_cast<std::uint32_t>(c - 'A' + 10);
-      else error("bad \\u escape");
-    }
-    return v;
-  }
-  std::string string() {
-    expect('"');
-    std::string out;
-    while (true) {
-      if (i_ >= s_.size()) error("unterminated string");
-      const char c = s_[i_++];
-      if (c == '"') return out;
-      if (static_cast<unsigned char>(c) < 0x20) error("control character in string");
-      if (c != '\\') {
-        out += c;
-        continue;
-      }
-      if (i_ >= s_.size()) error("unterminated escape");
-      const char e = s_[i_++];
-      switch (e) {
-        case '"': case '\\': case '/': out += e; break;
-        case 'b': out += '\b'; break;
-        case 'f': out += '\f'; break;
-        case 'n': out += '\n'; break;
-        case 'r': out += '\r'; break;
-        case 't': out += '\t'; break;
-        case 'u': {
-          std::uint32_t cp = hex4();
-          if (cp >= 0xD800 && cp < 0xDC00) {  // surrogate pair
-            if (!literal("\\u")) error("lone surrogate");
-            const std::uint32_t lo = hex4();
-            if (lo < 0xDC00 || lo >= 0xE000) error("bad surrogate pair");
-            cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
-          }
-          utf8(out, cp);
-          break;
-        }
-        default: error("unsupported escape");
-      }
-    }
-  }
-  std::string number() {
-    const std::size_t b = i_;
-    if (i_ < s_.size() && s_[i_] == '-') ++i_;
-    auto digits = [&] {
-      const std::size_t d = i_;
-      while (i_ < s_.size() && s_[i_] >= '0' && s_[i_] <= '9') ++i_;
-      return i_ > d;
-    };
-    if (!digits()) error("bad number");
-    if (i_ < s_.size() && s_[i_] == '.') {
-      ++i_;
-      if (!digits()) error("bad number");
-    }
-    if (i_ < s_.size() && (s_[i_] == 'e' || s_[i_] == 'E')) {
-      ++i_;
-      if (i_ < s_.size() && (s_[i_] == '+' || s_[i_] == '-')) ++i_;
-      if (!digits()) error("bad number");
-    }
-    return std::string(s_.substr(b, i_ - b));
-  }
-  Json value(int depth) {
-    if (depth > kMaxDepth) error("nesting too deep");
-    ws();
-    if (i_ >= s_.size()) error("unexpected end");
-    Json v;
-    const char c = s_[i_];
-    if (c == '{') {
-      ++i_;
-      v.kind = Json::Object;
-      if (take('}')) return v;
-      do {
-        ws();
-        std::string key = string();
-        expect(':');
-        v.members.emplace_back(std::move(key), value(depth + 1));
-      } while (take(','));
-      expect('}');
-    } else if (c == '[') {
-      ++i_;
-      v.kind = Json::Array;
-      if (take(']')) return v;
-      do v.items.push_back(value(depth + 1));
-      while (take(','));
-      expect(']');
-    } else if (c == '"') {
-      v.kind = Json::String;
-      v.text = string();
-    } else if (literal("true")) {
-      v.kind = Json::Bool, v.b = true;
-    } else if (literal("false")) {
-      v.kind = Json::Bool;
-    } else if (literal("null")) {
-      v.kind = Json::Null;
-    } else {
-      v.kind = Json::Number;
-      v.text = number();
-    }
-    return v;
-  }
-};
-
-std::string read_text(const std::filesystem::path& path, const char* what) {
-  std::ifstream in(path, std::ios::binary);
-  if (!in) fail(std::string("failed to open ") + what + ": " + path.string());
-  std::string text((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
-  if (in.bad()) fail(std::string("failed to read ") + what + ": " + path.string());
-  return text;
-}
-
 // ---- field access (required fields throw, optional ones default) --------------------
 
-// A non-negative integer literal (no sign, fraction or exponent).
-bool as_u64(const Json& v, std::uint64_t& out) {
-  if (v.kind != Json::Number || v.text.empty()) return false;
-  std::uint64_t x = 0;
-  for (const char c : v.text) {
-    if (c < '0' || c > '9') return false;
-    const std::uint64_t d = static_cast<std::uint64_t>(c - '0');
-    if (x > (UINT64_MAX - d) / 10u) return false;
-    x = x * 10u + d;
-  }
-  out = x;
-  return true;
-}
+using json::Json;
+using json::Reader;
+using json::as_u64;
+using json::read_text;
 
 const Json& need(const Json& obj, const char* key) {
   const Json* v = obj.find(key);
@@ -503,6 +307,18 @@ IQManifest load_iq_manifest(const std::filesystem::path& path) {
   }
   if (m.tensors.empty()) fail("IQ manifest contains no tensors");
   return m;
+}
+
+PackManifestKind pack_manifest_kind(const std::filesystem::path& path) {
+  const Json doc = Reader(read_text(path, "manifest")).document();
+  const std::string producer = opt_str(doc, "path");
+  if (producer == "q4k_resident_pack") return PackManifestKind::Q4K;
+  if (producer == "iq_resident_pack" || producer == "q5k_resident_pack") return PackManifestKind::RawBlocks;
+  if (!producer.empty()) fail("unknown pack producer " + producer + ": " + path.string());
+  const auto& recs = tensor_records(doc, "manifest");
+  if (!recs.empty() && recs.front().find("metadata_path") != nullptr) return PackManifestKind::Q4K;
+  if (!recs.empty() && recs.front().find("type") != nullptr) return PackManifestKind::RawBlocks;
+  fail("cannot tell the kind of manifest " + path.string());
 }
 
 IQManifestTensor select_iq_tensor(const IQManifest& manifest, const std::string& name) {

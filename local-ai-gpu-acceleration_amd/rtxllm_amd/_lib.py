@@ -54,6 +54,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_llama_graph_replay_span": [_P, _U, _S],
     "rtxllm_llama_launch_stage": [_P, _U, c_int, _S],
     "rtxllm_llama_load_packs": [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
+    "rtxllm_llama_load_pack_set": [_P, _P, _U, ctypes.c_char_p, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_memory": [_P, _P, _P, _P],
     "rtxllm_llama_status": [_P, _P, _S],
     "rtxllm_llama_clear_status": [_P, _S],
@@ -85,8 +86,23 @@ for _name in (
 ):
     _LAUNCH_SIGS[_name] = [_P, _P, _P, _P, _P, _P, _U, _U, _U, _U, _U, _S]
 
+
+
+class PackOptions(ctypes.Structure):
+    """rtxllm_pack_options (include/rtxllm/pack_producer.h)."""
+    _fields_ = [("q4k_policy", ctypes.c_char_p), ("write_blocks", c_int), ("types", ctypes.c_char_p),
+                ("names", ctypes.c_char_p), ("layer", c_int), ("limit", c_uint64)]
+
+
+_C = ctypes.c_char_p
 # name -> (restype, argtypes) for host helpers.
 _HOST_SIGS: dict[str, tuple] = {
+    "rtxllm_gguf_pack": (c_int, [_C, _C, ctypes.POINTER(PackOptions), _C, c_size_t, _C, c_size_t]),
+    "rtxllm_pack_tensor": (c_int, [_C, _C, _C, _C, c_int, _C, c_size_t, _C, c_size_t]),
+    "rtxllm_gguf_tensor_plan": (c_int, [_C, _C, c_size_t, _C, c_size_t]),
+    "rtxllm_pack_tensor_shape": (c_int, [_C, _P, c_uint32, _P, _P, _P, _C, c_size_t]),
+    "rtxllm_pack_tensor_role": (c_int, [_C, _P, _C, c_size_t]),
+    "rtxllm_pack_sanitize_label": (c_int, [_C, _C, c_size_t]),
     "rtxllm_format_payload_block_bytes": (c_uint32, [c_int]),
     "rtxllm_format_meta_block_bytes": (c_uint32, [c_int]),
     "rtxllm_xq_bytes": (c_size_t, [c_uint32]),
@@ -161,4 +177,5 @@ def check(name: str, code: int) -> None:
         raise HipError(name, code)
 
 
-__all__ = ["lib", "probe_lib", "check", "HipError", "exported_names", "LIB_PATH", "PROBE_LIB_PATH", "c_uint16"]
+__all__ = ["lib", "probe_lib", "check", "HipError", "exported_names", "LIB_PATH", "PROBE_LIB_PATH", "PackOptions",
+           "c_uint16"]

@@ -11,11 +11,13 @@ file) and may carry alignment padding (tools/bench/gguf_tensor_plan.py:53-80,
 gguf_block_formats.py:47-80): padding >= alignment is refused.
 
 to_packs() turns the quantized tensors of a GGUF Llama model into the resident
-packs and manifests the decode runner loads (rtxllm_llama_load_packs): Q4_K
-tensors into the chosen split layout, IQ2_S / IQ3_S / Q5_K as raw blocks,
-with the tensors' absolute file offsets in the tensor plan. The fp32 norm
-vectors are returned by norms() for upload; llama_shape() reads the model
-shape from the llama.* metadata keys.
+packs and manifests the decode runner loads (rtxllm_llama_load_pack_set),
+through the library's C++ producer (rtxllm_gguf_pack, producer.py): Q4_K
+tensors into the chosen split layout, IQ2_S / IQ3_S / Q5_K as raw blocks, one
+manifest per producer in the reference producers' form, with the tensors'
+absolute file offsets in the tensor plan. The fp32 norm vectors are returned
+by norms() for upload; llama_shape() reads the model shape from the llama.*
+metadata keys.
 """
 
 from __future__ import annotations
@@ -319,16 +321,15 @@ def model_formats(g: GGUF, policy: str = "split-native") -> dict:
 
 
 def to_packs(g: GGUF, out_dir, policy: str = "split-native", write_blocks: bool = True) -> dict[str, Path]:
-    """Resident packs + manifests of every Q4_K / Q5_K / IQ2_S / IQ3_S tensor
-    (manifest.write_packs), with the tensors' absolute file offsets."""
-    tensors = []
-    for t in g.tensors:
-        if t.type not in PACK_FORMATS:
-            continue
-        tensors.append(M.Tensor(t.name, PACK_FORMATS[t.type], t.rows, t.cols, g.data(t),
-                                offset=g.data_offset + t.offset))
-    name = g.path.name if g.path is not None else "model.gguf"
-    return M.write_packs(Path(out_dir), tensors, policy=policy, write_blocks=write_blocks, model=name)
+    """Resident packs + manifests of every Q4_K / Q5_K / IQ2_S / IQ3_S tensor of
+    a file-backed GGUF, written by the C++ producer (producer.pack_gguf):
+    returns the paths of "tensor_plan" and of the "q4k_manifest",
+    "iq_manifest" and "q5k_manifest" written."""
+    if g.path is None:
+        raise ValueError("to_packs needs a file-backed GGUF")
+    from . import producer
+
+    return producer.pack_gguf(g.path, out_dir, policy=policy, write_blocks=write_blocks)
 
 
 def norms(g: GGUF) -> dict[tuple[str, int], np.ndarray]:
@@ -353,9 +354,9 @@ def norms(g: GGUF) -> dict[tuple[str, int], np.ndarray]:
 def load_into(model, g: GGUF, work_dir, policy: str = "split-native") -> dict[str, Path]:
     """Fill a rtxllm_amd.llama.Llama created with llama_shape(g) and
     model_formats(g, policy): packs written to work_dir and loaded through
-    rtxllm_llama_load_packs, norm vectors uploaded. Returns the pack paths."""
+    rtxllm_llama_load_pack_set, norm vectors uploaded. Returns the pack paths."""
     paths = to_packs(g, work_dir, policy=policy)
-    model.load_packs(paths.get("q4k_manifest"), paths.get("iq_manifest"), work_dir)
+    model.load_pack_set([p for k, p in paths.items() if k.endswith("_manifest")])
     for (role, layer), v in norms(g).items():
         model.upload(role, v, layer=layer)
     return paths

@@ -164,6 +164,19 @@ class Llama:
             from ._lib import HipError
             raise HipError(f"rtxllm_llama_load_packs: {err.value.decode(errors='replace')}", rc)
 
+    def load_pack_set(self, manifests, payload_root=None) -> None:
+        """Fill the weights from any number of manifests, each read by the loader
+        its producer needs (rtxllm_llama_load_pack_set)."""
+        paths = [str(p).encode() for p in manifests]
+        arr = (ctypes.c_char_p * max(1, len(paths)))(*paths)
+        err = ctypes.create_string_buffer(1024)
+        rc = lib().rtxllm_llama_load_pack_set(self.h, ctypes.cast(arr, c_void_p), len(paths),
+                                              None if payload_root is None else str(payload_root).encode(), err,
+                                              len(err))
+        if rc != 0:
+            from ._lib import HipError
+            raise HipError(f"rtxllm_llama_load_pack_set: {err.value.decode(errors='replace')}", rc)
+
     def memory(self) -> dict:
         """The create-time admission figures: required, usable and arena bytes."""
         req, use, arena = c_size_t(), c_size_t(), c_size_t()

@@ -1,10 +1,14 @@
-"""Resident-pack producer: writes GGUF tensors (raw blocks in memory) as the
-pack files and manifest.json records of the reference's pack producers
-(tools/bench/q4k_resident_pack.py:170-222 for Q4_K, iq_resident_pack.py:115-147
-for IQ2_S / IQ3_S / Q5_K), plus a GGUF tensor plan
-(tools/bench/gguf_tensor_plan.py: name, type, dimensions, span_bytes,
-absolute_offset). The decode runner reads them back through
-rtxllm_llama_load_packs (include/rtxllm/pack_manifest.h loaders).
+"""Pack writer for tensors held in memory (a model's own weights, synthetic
+blocks): the pack files and manifest.json records of the reference's pack
+producers (tools/bench/q4k_resident_pack.py:170-222 for Q4_K,
+iq_resident_pack.py:115-147 for IQ2_S / IQ3_S, q5k_resident_pack.py:93-120 for
+Q5_K, with their runtime_kernel labels and file labels), plus a GGUF tensor
+plan (tools/bench/gguf_tensor_plan.py: name, type, dimensions, span_bytes,
+absolute_offset). GGUF files are packed by the library's C++ producer
+(producer.pack_gguf); this writer serves callers without a file. It writes
+two manifests, Q4_K and raw blocks (IQ2_S / IQ3_S / Q5_K together, which the
+raw-block loader accepts), read back through rtxllm_llama_load_packs
+(include/rtxllm/pack_manifest.h loaders).
 
 Q4_K tensors get the payload + metadata streams of one split layout (the
 policy) and, with write_blocks, the raw blocks file. Checksums are byte sums;
@@ -44,7 +48,8 @@ def auto_policy(rows: int, cols: int, lossy: bool = False) -> str:
     up to 4096 blocks, else predecoded) is an RTX 3060 measurement; on MI355X
     both are slower than split-native."""
     return "split-half" if lossy and rows * cols // F.BLOCK_VALUES > 65536 else "split-native"
-KERNEL_LABELS = {"IQ2_S": "iq2s_raw_block_probe", "IQ3_S": "iq3s_raw_block_probe", "Q5_K": "q5k_raw_block_probe"}
+# runtime_kernel of the raw-block producers (iq_resident_pack.py:124-127, q5k_resident_pack.py:119)
+KERNEL_LABELS = {"IQ2_S": "iq2s_raw_block_probe", "IQ3_S": "iq3s_raw_block_probe", "Q5_K": "q5_k_raw_pending"}
 
 
 @dataclass
@@ -60,7 +65,8 @@ class Tensor:
 
 
 def _label(name: str) -> str:
-    return re.sub(r"[^A-Za-z0-9_.-]+", "_", name)
+    """File label of a tensor name (tools/bench/native_harness.py:126-128)."""
+    return re.sub(r"[^A-Za-z0-9_.-]+", "_", name.strip()).strip("._-") or "native"
 
 
 def _checksum(a: np.ndarray) -> int:
@@ -143,7 +149,7 @@ def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-nativ
     if q4k:
         paths["q4k_manifest"] = out_dir / "q4k_manifest.json"
         paths["q4k_manifest"].write_text(json.dumps({
-            "generated_at": stamp, "model": model, "tensor_plan": str(paths["tensor_plan"]), "output_dir": str(out_dir),
+            "path": "q4k_resident_pack", "generated_at": stamp, "model": model, "tensor_plan": str(paths["tensor_plan"]), "output_dir": str(out_dir),
             "policy": policy, "tensor_count": len(q4k),
             "resident_bytes": sum(t["resident_bytes"] for t in q4k),
             "payload_bytes": sum(t["payload_bytes"] for t in q4k),
@@ -151,7 +157,7 @@ def write_packs(out_dir: Path, tensors: list[Tensor], policy: str = "split-nativ
     if raw:
         paths["iq_manifest"] = out_dir / "iq_manifest.json"
         paths["iq_manifest"].write_text(json.dumps({
-            "generated_at": stamp, "model": model, "tensor_plan": str(paths["tensor_plan"]),
+            "path": "iq_resident_pack", "generated_at": stamp, "model": model, "tensor_plan": str(paths["tensor_plan"]),
             "types": sorted({t["type"] for t in raw}), "tensor_count": len(raw),
             "source_bytes": sum(t["source_bytes"] for t in raw), "payload_bytes": sum(t["payload_bytes"] for t in raw),
             "resident_bytes": sum(t["resident_bytes"] for t in raw), "tensors": raw}, indent=1))

@@ -135,8 +135,52 @@ int load_mode(char** argv) {
   }
 }
 
+// --load-set TENSOR_PLAN ROOT MANIFEST...: each manifest read by the loader its
+// producer needs (pack_manifest_kind), validated against the plan, every pack
+// file's size and checksum checked; one line per tensor, as --load prints.
+int load_set_mode(int argc, char** argv) {
+  try {
+    const std::filesystem::path plan = argv[2], root = argv[3];
+    auto under = [&](const std::filesystem::path& p) { return p.is_absolute() ? p : root / p; };
+    int bad = 0;
+    for (int a = 4; a < argc; ++a) {
+      if (pack_manifest_kind(argv[a]) == PackManifestKind::Q4K) {
+        const auto q = load_q4k_manifest(argv[a]);
+        validate_q4k_manifest_tensors_against_plan(select_q4k_tensors(q, {}, 0), plan);
+        for (const auto& t : q.tensors) {
+          const bool ok =
+              byte_checksum(load_binary_file(under(t.payload_path), t.payload_bytes, "payload")) ==
+                  t.payload_checksum &&
+              byte_checksum(load_binary_file(under(t.metadata_path), t.metadata_bytes, "metadata")) ==
+                  t.metadata_checksum &&
+              (t.blocks_path.empty() ||
+               byte_checksum(load_binary_file(under(t.blocks_path), t.source_bytes, "blocks")) == t.source_checksum);
+          std::printf("q4k %s layer=%d role=%s rows=%u cols=%u policy=%s ok=%d\n", t.name.c_str(), t.layer,
+                      t.role.c_str(), t.rows, t.cols, t.policy.c_str(), ok ? 1 : 0);
+          bad += ok ? 0 : 1;
+        }
+      } else {
+        const auto i = load_iq_manifest(argv[a]);
+        validate_iq_manifest_tensors_against_plan(i.tensors, plan);
+        for (const auto& t : i.tensors) {
+          const bool ok =
+              byte_checksum(load_binary_file(under(t.payload_path), t.payload_bytes, "payload")) == t.payload_checksum;
+          std::printf("raw %s type=%s layer=%d blocks=%llu kernel=%s ok=%d\n", t.name.c_str(), t.type.c_str(),
+                      t.layer, static_cast<unsigned long long>(t.block_count), t.runtime_kernel.c_str(), ok ? 1 : 0);
+          bad += ok ? 0 : 1;
+        }
+      }
+    }
+    return bad == 0 ? 0 : 1;
+  } catch (const std::exception& e) {
+    std::printf("error %s\n", e.what());
+    return 1;
+  }
+}
+
 int main(int argc, char** argv) {
   if (argc == 6 && std::string(argv[1]) == "--load") return load_mode(argv);
+  if (argc >= 5 && std::string(argv[1]) == "--load-set") return load_set_mode(argc, argv);
   g_dir = std::filesystem::temp_directory_path() / ("rtxllm_selftest_" + std::to_string(::getpid()));
   std::filesystem::create_directories(g_dir);
 

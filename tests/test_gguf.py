@@ -161,9 +161,11 @@ def test_packs_from_gguf_pass_the_loaders(selftest, tmp_path, policy):
     for t in g.tensors:
         if t.type in G.PACK_FORMATS:
             assert plan[t.name]["absolute_offset"] == g.data_offset + t.offset
-    r = subprocess.run([str(selftest), "--load", str(paths["q4k_manifest"]), str(paths["iq_manifest"]),
-                        str(paths["tensor_plan"]), str(out)], capture_output=True, text=True, timeout=120)
+    manifests = [str(paths[k]) for k in ("q4k_manifest", "iq_manifest", "q5k_manifest")]
+    r = subprocess.run([str(selftest), "--load-set", str(paths["tensor_plan"]), str(out)] + manifests,
+                       capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
+    assert len(r.stdout.splitlines()) == 16
 
 
 def test_cli_inspect(tmp_path, capsys):

@@ -4,8 +4,11 @@ own synthetic weights (q / k / v split out of the stacked rows, gate / up out
 of the interleaved rows, Q4_K down re-joined into raw blocks and packed
 split-native) load back bit-identically into a second model, whose decode
 step then matches the first bit for bit; a missing tensor, a pack layout
-other than the configured one and a corrupted file are refused. All calls go
-through the C-ABI."""
+other than the configured one and a corrupted file are refused. A GGUF file
+goes through the library's C++ producer (one manifest per producer, in the
+reference producers' form) and rtxllm_llama_load_pack_set, which also refuses
+a tensor named twice and an unknown producer. All calls go through the
+C-ABI."""
 
 from __future__ import annotations
 
@@ -151,4 +154,33 @@ def test_gguf_file_loads_bit_identical_and_step_matches(source, tmp_path):
     torch.cuda.synchronize()
     assert np.array_equal(m.download("logits", np.float32).view(np.uint32),
                           source.download("logits", np.float32).view(np.uint32))
+    m.close()
+
+
+def test_pack_set_refuses_duplicates_and_unknown_producers(source, tmp_path):
+    """rtxllm_llama_load_pack_set: a tensor named by two manifests and a
+    manifest of an unknown producer are refused, and the weights stay as they
+    were; the same manifests without the duplicate load bit-identically."""
+    import json
+
+    tensors = gguf_tensors(source)
+    paths = M.write_packs(tmp_path / "a", tensors, absolute_paths=True)
+    extra = M.write_packs(tmp_path / "b", [t for t in tensors if t.name == "output.weight"], absolute_paths=True)
+    m = Llama(SMALL)
+    m.synth_weights(SEED + 1)
+    torch.cuda.synchronize()
+    before = m.download("lm_head", np.uint8)
+    with pytest.raises(HipError, match="tensor in two manifests: output.weight"):
+        m.load_pack_set([paths["q4k_manifest"], paths["iq_manifest"], extra["iq_manifest"]])
+    doc = json.loads(paths["iq_manifest"].read_text())
+    doc["path"] = "q6k_resident_pack"
+    odd = tmp_path / "odd.json"
+    odd.write_text(json.dumps(doc))
+    with pytest.raises(HipError, match="unknown pack producer q6k_resident_pack"):
+        m.load_pack_set([paths["q4k_manifest"], odd])
+    assert np.array_equal(m.download("lm_head", np.uint8), before)
+    m.load_pack_set([paths["q4k_manifest"], paths["iq_manifest"]])
+    for l in range(SMALL.n_layers):
+        for r in WEIGHT_REGIONS:
+            assert np.array_equal(m.download(r, np.uint8, layer=l), source.download(r, np.uint8, layer=l)), (l, r)
     m.close()
