@@ -69,6 +69,31 @@ __device__ __forceinline__ float dequant_value(const std::uint8_t* p, const std:
     }
   }
 }
+
+// Values [16 t, 16 t + 16) of a Q5_K block (t in [0, 16)) from three aligned
+// 16-byte loads: the head (d, dmin, scales), the 16 qh bytes and the 16 qs
+// bytes the run uses (the run lies in one 32-value sub-block). Same values,
+// bit for bit, as dequant_value<Q5K> for each v in the run. The block must be
+// 16-byte aligned (176-byte blocks of a 16-byte aligned table are).
+__device__ __forceinline__ void dequant_q5k_run16(const std::uint8_t* blk, std::uint32_t t, float out[16]) {
+  const std::uint32_t v0 = 16u * t, g = v0 >> 6, high = (v0 & 63u) >= 32u ? 1u : 0u, lane0 = v0 & 31u;
+  const uint4 head = *reinterpret_cast<const uint4*>(blk);
+  const uint4 qh4 = *reinterpret_cast<const uint4*>(blk + 16u + lane0);
+  const uint4 qs4 = *reinterpret_cast<const uint4*>(blk + 48u + 32u * g + lane0);
+  const float d = f16_bits_to_f32(static_cast<std::uint16_t>(head.x & 0xFFFFu));
+  const float dmin = f16_bits_to_f32(static_cast<std::uint16_t>(head.x >> 16));
+  std::uint32_t sc, mn;
+  scale_min_k4(static_cast<int>(2u * g + high), head.y, head.z, head.w, sc, mn);
+  const std::uint32_t qh[4] = {qh4.x, qh4.y, qh4.z, qh4.w}, qs[4] = {qs4.x, qs4.y, qs4.z, qs4.w};
+  const std::uint32_t hbit = 2u * g + high;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const std::uint32_t packed = (qs[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    const std::uint32_t low = high ? (packed >> 4) : (packed & 15u);
+    const std::uint32_t quant = low + (((((qh[j >> 2] >> (8 * (j & 3))) & 0xFFu) >> hbit) & 1u) ? 16u : 0u);
+    out[j] = d * static_cast<float>(sc) * static_cast<float>(quant) - dmin * static_cast<float>(mn);
+  }
+}
 #pragma clang fp contract(on)
 
 }  // namespace rtxllm

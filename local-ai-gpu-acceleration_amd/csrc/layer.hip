@@ -221,11 +221,10 @@ __global__ __launch_bounds__(1024) void embed_q5k_kernel(const std::uint8_t* __r
     if (table != nullptr) {
       const std::size_t row = token[0] < vocab ? token[0] : vocab - 1u;
       const std::uint8_t* blk = table + (row * (cols / 256u) + c0 / 256u) * 176u;
+      dequant_q5k_run16(blk, (c0 & 255u) / 16u, v);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        v[j] = dequant_value<RTXLLM_FMT_Q5K>(blk, nullptr, (c0 & 255u) + j);
-        h[c0 + j] = v[j];
-      }
+      for (int j = 0; j < 16; j += 4)
+        *reinterpret_cast<float4*>(h + c0 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
     } else {
 #pragma unroll
       for (int j = 0; j < 16; ++j) v[j] = h[c0 + j];
@@ -624,6 +623,9 @@ hipError_t launch_embed_q5k(const std::uint8_t* table, std::uint32_t cols, std::
                             const std::uint32_t* token, float* h, const float* wnorm, void* xq, float* sumsq,
                             std::uint32_t nslots, hipStream_t stream) {
   if (cols == 0u || (cols % 256u) != 0u || cols > 16384u || nslots == 0u || vocab == 0u) return hipErrorInvalidValue;
+  // the gather reads 16-byte fields of the 176-byte blocks and writes h by float4
+  if ((reinterpret_cast<std::uintptr_t>(table) | reinterpret_cast<std::uintptr_t>(h)) % 16u != 0u)
+    return hipErrorInvalidValue;
   const std::uint32_t threads = ((cols / kXGroup + 63u) / 64u) * 64u;  // whole waves
   hipLaunchKernelGGL(embed_q5k_kernel, dim3(1), dim3(threads), 0, stream, table, cols, vocab, token, h, wnorm,
                      xq_out(xq, cols), sumsq, nslots);

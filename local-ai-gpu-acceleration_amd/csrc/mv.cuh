@@ -330,14 +330,12 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
     const u32x2 q = bld_u64<P>(rp, u.o[0], 64u * sp);
     r.a[0] = q.x, r.a[1] = q.y;
-    const std::uint32_t hs = bld_u16<P>(rp, u.o[1], 16u * sp);
-    r.c[1] = hs & 0xFFu, r.c[2] = hs >> 8;
+    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8, kept in one register
     r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S_UNITS) {
     const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rp, u.o[0], 96u * sp, P);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z;
-    const std::uint32_t hs = bld_u16<P>(rp, u.o[1], 16u * sp);
-    r.c[1] = hs & 0xFFu, r.c[2] = hs >> 8;
+    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8
     r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
   } else if constexpr (fmt_is_iq2s(FMT)) {
     r.c[0] = bld_u16<P>(rp, u.o[0], sp);
@@ -391,6 +389,14 @@ __device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uin
   s1 = d * static_cast<float>((sc >> 8) & 0xFFu);
   m0 = dmin * static_cast<float>(mn & 0xFFu);
   m1 = dmin * static_cast<float>((mn >> 8) & 0xFFu);
+}
+
+// The IQ scale byte: beside qh in one 16-bit field in the unit layouts, its
+// own byte in the GGUF layouts. (qh bits above bit 7 never reach an index.)
+template <int FMT>
+__device__ __forceinline__ std::uint32_t iq_scale_byte(const UnitRaw& r) {
+  if constexpr (fmt_is_units(FMT)) return r.c[1] >> 8;
+  else return r.c[2];
 }
 
 // IQ units in two phases, so the LDS lookups of one row can be in flight while
@@ -467,12 +473,13 @@ __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, con
   const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   if constexpr (fmt_is_iq2s(FMT)) {
     // d * (0.5 + n) / 4 * s = d * (n * s / 4 + s / 8)
-    const float f0 = __builtin_fmaf(static_cast<float>(r.c[2] & 15u), ls.a0, ls.b0);
-    const float f1 = __builtin_fmaf(static_cast<float>(r.c[2] >> 4), ls.a1, ls.b1);
+    const std::uint32_t sc = iq_scale_byte<FMT>(r);
+    const float f0 = __builtin_fmaf(static_cast<float>(sc & 15u), ls.a0, ls.b0);
+    const float f1 = __builtin_fmaf(static_cast<float>(sc >> 4), ls.a1, ls.b1);
     return d * __builtin_fmaf(f1, D1, f0 * D0);
   } else {
     // d * (1 + 2 n) for the whole unit
-    const float m = __builtin_fmaf(static_cast<float>((r.c[2] >> ls.nib_shift) & 15u), 2.0f, 1.0f);
+    const float m = __builtin_fmaf(static_cast<float>((iq_scale_byte<FMT>(r) >> ls.nib_shift) & 15u), 2.0f, 1.0f);
     return (d * m) * __builtin_fmaf(x1.s, D1, x0.s * D0);
   }
 }
