@@ -53,6 +53,15 @@ typedef struct rtxllm_llama rtxllm_llama;
  * first (include/rtxllm/admission.h): hipErrorOutOfMemory when weights + KV
  * + workspace + graph memory exceed the device's free bytes. */
 hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out);
+
+/* The admission decision rtxllm_llama_create would make, without allocating:
+ * *admitted = 1 or 0, the bytes the model needs and the device bytes it is
+ * measured against (free bytes less guard_bytes: the reference runner's
+ * --wddm-guard-mib, runtime/core/scheduler/admission.h:10-65), and the decision's reason
+ * (at most reason_len bytes with the NUL). hipErrorInvalidValue for a config
+ * create refuses. */
+hipError_t rtxllm_llama_admission(const rtxllm_llama_config* cfg, size_t guard_bytes, int* admitted,
+                                  size_t* required_bytes, size_t* usable_bytes, char* reason, size_t reason_len);
 void rtxllm_llama_destroy(rtxllm_llama* m);
 
 /* Device pointer (and size) of a named region, or NULL. Per layer: "qkv",

@@ -97,6 +97,7 @@ int rtxllm_pack_sanitize_label(const char* name, char* label, size_t label_len);
 
 #include <filesystem>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace rtxllm {
@@ -120,7 +121,20 @@ struct GgufHeader {
   std::uint64_t alignment = 32;
   std::string architecture;  // general.architecture, when a string
   std::string model_name;    // general.name, when a string
+  // every scalar numeric metadata value (integer, float or bool types) by key
+  std::vector<std::pair<std::string, double>> numbers;
   std::vector<GgufTensorInfo> tensors;
+  // numbers[key], or fallback when absent
+  double number(const std::string& key, double fallback) const {
+    for (const auto& kv : numbers)
+      if (kv.first == key) return kv.second;
+    return fallback;
+  }
+  const GgufTensorInfo* tensor(const std::string& name) const {
+    for (const auto& t : tensors)
+      if (t.name == name) return &t;
+    return nullptr;
+  }
 };
 
 struct TensorPlanRow {

@@ -168,10 +168,14 @@ hipError_t synth_tensor(rtxllm_llama* m, const std::string& name, int fmt, std::
 
 }  // namespace
 
-extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out) {
-  if (cfg == nullptr || out == nullptr) return hipErrorInvalidValue;
-  *out = nullptr;
-  const rtxllm_llama_config& c = *cfg;
+namespace {
+
+// The model's plan without allocating: the validated config, the derived sizes
+// in m, the arena specs, and the strict admission decision (m.admission) of
+// weights, KV cache, workspace and the step graph's memory against the
+// device's free bytes less guard_bytes.
+hipError_t plan_model(const rtxllm_llama_config& c, std::size_t guard_bytes, rtxllm_llama* m,
+                      std::vector<ArenaSpec>& specs) {
   const bool shapes_ok = c.hidden != 0u && c.hidden % 256u == 0u && c.hidden <= 16384u && c.n_heads != 0u &&
                          c.n_kv_heads != 0u && c.n_heads % c.n_kv_heads == 0u && c.n_heads / c.n_kv_heads <= 8u &&
                          (c.n_heads * rtxllm::kHeadDim) % 256u == 0u && c.ffn != 0u && c.ffn % 256u == 0u &&
@@ -195,8 +199,6 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
       return hipErrorInvalidValue;
   }
 
-  std::unique_ptr<rtxllm_llama> m(new (std::nothrow) rtxllm_llama());
-  if (!m) return hipErrorOutOfMemory;
   m->cfg = c;
   m->q_rows = c.n_heads * rtxllm::kHeadDim;
   m->kv_rows = c.n_kv_heads * rtxllm::kHeadDim;
@@ -218,7 +220,7 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
 
   const std::size_t kv_halves =
       B * m->pages_per_seq * c.n_kv_heads * c.page_size * rtxllm::kHeadDim;
-  std::vector<ArenaSpec> specs;
+  specs.clear();
   for (std::uint32_t l = 0; l < c.n_layers; ++l) {
     add_tensor(specs, layer_name("qkv", l), c.fmt_qkv, m->q_rows + 2u * m->kv_rows, c.hidden);
     add_tensor(specs, layer_name("o", l), c.fmt_o, c.hidden, m->q_rows);
@@ -299,9 +301,43 @@ extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm
     std::size_t free_b = 0, total_b = 0;
     const hipError_t mi = hipMemGetInfo(&free_b, &total_b);
     if (mi != hipSuccess) return mi;
-    m->admission = rtxllm::decide_admission(rtxllm::ResidencyPolicy::Strict, rtxllm::MemoryBudget{free_b, 0}, req);
-    if (!m->admission.admit) return hipErrorOutOfMemory;
+    m->admission =
+        rtxllm::decide_admission(rtxllm::ResidencyPolicy::Strict, rtxllm::MemoryBudget{free_b, guard_bytes}, req);
   }
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" hipError_t rtxllm_llama_admission(const rtxllm_llama_config* cfg, size_t guard_bytes, int* admitted,
+                                             size_t* required_bytes, size_t* usable_bytes, char* reason,
+                                             size_t reason_len) {
+  if (cfg == nullptr) return hipErrorInvalidValue;
+  std::unique_ptr<rtxllm_llama> m(new (std::nothrow) rtxllm_llama());
+  if (!m) return hipErrorOutOfMemory;
+  std::vector<ArenaSpec> specs;
+  const hipError_t st = plan_model(*cfg, guard_bytes, m.get(), specs);
+  if (st != hipSuccess) return st;
+  if (admitted != nullptr) *admitted = m->admission.admit ? 1 : 0;
+  if (required_bytes != nullptr) *required_bytes = m->admission.required_bytes;
+  if (usable_bytes != nullptr) *usable_bytes = m->admission.usable_bytes;
+  if (reason != nullptr && reason_len > 0) std::snprintf(reason, reason_len, "%s", m->admission.reason.c_str());
+  return hipSuccess;
+}
+
+extern "C" hipError_t rtxllm_llama_create(const rtxllm_llama_config* cfg, rtxllm_llama** out) {
+  if (cfg == nullptr || out == nullptr) return hipErrorInvalidValue;
+  *out = nullptr;
+  const rtxllm_llama_config& c = *cfg;
+  std::unique_ptr<rtxllm_llama> m(new (std::nothrow) rtxllm_llama());
+  if (!m) return hipErrorOutOfMemory;
+  std::vector<ArenaSpec> specs;
+  {
+    const hipError_t pst = plan_model(c, 0u, m.get(), specs);
+    if (pst != hipSuccess) return pst;
+  }
+  if (!m->admission.admit) return hipErrorOutOfMemory;
+  const std::size_t B = m->batch;
   try {
     m->arena.initialize(specs);
     m->arena.reset();

@@ -125,12 +125,34 @@ std::uint64_t scalar_bytes(std::uint32_t t) {
 }
 
 // Reads one metadata value: integers into *as_int (when non-null and the type
-// is an integer), strings into *as_string; arrays are walked and dropped.
+// is an integer), strings into *as_string, every scalar number (integers,
+// floats, bools) into *as_num; arrays are walked and dropped.
 void read_value(GgufReader& r, std::uint32_t type, int depth, std::int64_t* as_int, bool* is_int,
-                std::string* as_string, bool* is_string) {
+                std::string* as_string, bool* is_string, double* as_num = nullptr, bool* is_num = nullptr) {
   if (depth > 64) fail("GGUF metadata arrays nested too deep");
   if (is_int) *is_int = false;
   if (is_string) *is_string = false;
+  if (is_num) *is_num = false;
+  if (as_num != nullptr && (type == 6 || type == 7 || type == 12)) {
+    double v = 0.0;
+    if (type == 6) v = r.scalar<float>();
+    else if (type == 7) v = r.scalar<std::uint8_t>() != 0u ? 1.0 : 0.0;
+    else v = r.scalar<double>();
+    *as_num = v, *is_num = true;
+    return;
+  }
+  if (as_num != nullptr && (type <= 5u || type == 10u || type == 11u)) {
+    std::int64_t iv = 0;
+    bool ii = false;
+    read_value(r, type, depth, &iv, &ii, nullptr, nullptr);
+    if (type == 10u && !ii) {
+      *as_num = 18446744073709551615.0, *is_num = true;  // above INT64_MAX: only its size matters here
+      return;
+    }
+    if (as_int) *as_int = iv, *is_int = ii;
+    *as_num = static_cast<double>(iv), *is_num = true;
+    return;
+  }
   switch (type) {
     case 0: { const auto v = r.scalar<std::uint8_t>(); if (as_int) *as_int = v, *is_int = true; return; }
     case 1: { const auto v = r.scalar<std::int8_t>(); if (as_int) *as_int = v, *is_int = true; return; }
@@ -581,9 +603,11 @@ GgufHeader read_gguf_header(const fs::path& path) {
     const std::string key = r.string();
     const auto type = r.scalar<std::uint32_t>();
     std::int64_t iv = 0;
-    bool is_int = false, is_str = false;
+    bool is_int = false, is_str = false, is_num = false;
     std::string sv;
-    read_value(r, type, 0, &iv, &is_int, &sv, &is_str);
+    double nv = 0.0;
+    read_value(r, type, 0, &iv, &is_int, &sv, &is_str, &nv, &is_num);
+    if (is_num) h.numbers.emplace_back(key, nv);
     if (key == "general.alignment" && is_int) h.alignment = iv > 0 ? static_cast<std::uint64_t>(iv) : 32u;
     if (key == "general.architecture" && is_str) h.architecture = sv;
     if (key == "general.name" && is_str) h.model_name = sv;

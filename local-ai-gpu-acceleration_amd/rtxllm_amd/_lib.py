@@ -43,6 +43,7 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_matvec_batch_f32": [c_int, _P, _P, _P, _P, _U, _U, _U, _P, c_size_t, _S],
     "rtxllm_matvec_batch_noalloc": [c_int, _P, _P, _P, _P, _U, _U, _U, _S],
     "rtxllm_llama_create": [_P, _P],
+    "rtxllm_llama_admission": [_P, c_size_t, _P, _P, _P, ctypes.c_char_p, c_size_t],
     "rtxllm_llama_upload": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
     "rtxllm_llama_download": [_P, ctypes.c_char_p, _U, c_size_t, _P, c_size_t],
     "rtxllm_llama_synth_weights": [_P, c_uint64, _S],
