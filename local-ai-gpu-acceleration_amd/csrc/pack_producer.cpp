@@ -238,6 +238,13 @@ void write_file(const fs::path& p, const std::vector<std::uint8_t>& bytes) {
 std::vector<std::uint8_t> read_tensor_bytes(const fs::path& model, const TensorPlanRow& row, std::uint64_t expected,
                                             const char* what) {
   if (row.span_bytes < expected) fail(row.name + " span is smaller than expected " + what + " bytes");
+  std::error_code ec;
+  const std::uint64_t size = fs::file_size(model, ec);
+  if (ec) fail("failed to open model file: " + model.string());
+  if (row.absolute_offset > size || expected > size - row.absolute_offset) {  // before any allocation
+    const std::uint64_t got = row.absolute_offset < size ? size - row.absolute_offset : 0u;
+    fail("short read for " + row.name + ": expected " + std::to_string(expected) + ", got " + std::to_string(got));
+  }
   std::ifstream in(model, std::ios::binary);
   if (!in) fail("failed to open model file: " + model.string());
   in.seekg(static_cast<std::streamoff>(row.absolute_offset));

@@ -545,3 +545,18 @@ def test_pack_gguf_refusals(tmp_path):
         P.pack_gguf(path, tmp_path / "o", policy="fastest")
     with pytest.raises(ValueError, match="failed to stat"):
         P.pack_gguf(tmp_path / "missing.gguf", tmp_path / "o")
+
+
+def test_huge_rows_are_refused_before_allocating(tmp_path):
+    """A row whose dimensions claim far more data than the file holds is
+    refused from the file size, without reading or allocating that much."""
+    model = tmp_path / "m.bin"
+    model.write_bytes(bytes(1024))
+    out = tmp_path / "o"
+    out.mkdir()
+    huge = {"name": "w", "type": "Q4_K", "dimensions": [1 << 31, 1 << 20], "absolute_offset": 0,
+            "span_bytes": (1 << 63)}
+    with pytest.raises(ValueError, match="short read"):
+        P.pack_tensor(model, huge, out)
+    with pytest.raises(ValueError, match="short read"):
+        P.pack_tensor(model, dict(huge, type="IQ2_S", dimensions=[256, 1 << 40]), out)
