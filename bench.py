@@ -37,7 +37,7 @@ SEED = 0x5EED0004
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec-set", action="store_true")
@@ -118,15 +118,18 @@ def time_graph(torch, stream, fn, reps: int = 10) -> float:
 # ---- the decode step ------------------------------------------------------------
 
 def layer_weight_bytes(shape) -> dict:
+    """Algorithmic bytes of each matvec stage: rows * (cols / 256) * GGUF block
+    bytes + fp32 x (4 cols) + fp32 y (4 rows), the matvec figure of the
+    roofline (formats.algorithmic_bytes)."""
     from rtxllm_amd import formats as F
 
     H, q, kv, ff = shape.hidden, shape.n_heads * 128, shape.n_kv_heads * 128, shape.ffn
     return {
-        "qkv": (q + 2 * kv) * (H // 256) * F.GGUF_BLOCK_BYTES[F.IQ3S],
-        "o": H * (q // 256) * F.GGUF_BLOCK_BYTES[F.IQ3S],
-        "gate_up": 2 * ff * (H // 256) * F.GGUF_BLOCK_BYTES[F.IQ2S],
-        "down": H * (ff // 256) * F.GGUF_BLOCK_BYTES[F.Q4K_SPLIT_NATIVE],
-        "lm_head": shape.vocab * (H // 256) * F.GGUF_BLOCK_BYTES[F.Q5K],
+        "qkv": F.algorithmic_bytes(F.IQ3S, q + 2 * kv, H),
+        "o": F.algorithmic_bytes(F.IQ3S, H, q),
+        "gate_up": F.algorithmic_bytes(F.IQ2S, 2 * ff, H),
+        "down": F.algorithmic_bytes(F.Q4K_SPLIT_NATIVE, H, ff),
+        "lm_head": F.algorithmic_bytes(F.Q5K, shape.vocab, H),
     }
 
 
@@ -478,8 +481,8 @@ STAGE_UNITS = {  # 32-value weight units per launch at the 8B shapes (rows x col
     "qkv": 6144 * 4096 // 32, "o": 4096 * 4096 // 32, "gate_up": 28672 * 4096 // 32,
     "down": 4096 * 14336 // 32, "lm_head": 128256 * 4096 // 32,
 }
-STAGE_BYTES = {"qkv": 10813440, "attention": 16672768, "o": 7208960, "gate_up": 37617664, "down": 33030144,
-               "lm_head": 361168896}
+STAGE_BYTES = {"qkv": 10854400, "attention": 16672768, "o": 7241728, "gate_up": 37748736, "down": 33103872,
+               "lm_head": 361698304}  # layer_weight_bytes at the 8B shapes; attention: K + V at ~4070 positions
 
 
 def counter_summary(pmc_dirs) -> str:
@@ -636,8 +639,8 @@ def units_sweep(torch) -> dict:
     return out
 
 
-READ_SIZES = {"o": 7208960, "qkv": 10813440, "attention": 16777216, "iq2s_14336x4096": 18882560,
-              "down": 33030144, "gate_up": 37617664, "lm_head": 361168896}
+READ_SIZES = {"o": 7241728, "qkv": 10854400, "attention": 16777216, "iq2s_14336x4096": 18882560,
+              "down": 33103872, "gate_up": 37748736, "lm_head": 361698304}
 
 
 def read_ceiling(torch) -> dict:
