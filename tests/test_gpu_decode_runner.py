@@ -14,6 +14,8 @@ admission refuses the model, 3 when a gate fails; one JSON object on stdout.
   bit (tolerance 0).
 * A guard larger than the GPU's memory makes admission refuse: exit 2,
   "admitted": false, nothing allocated.
+* At the 32-layer 8B shapes (synthetic weights) every gate passes at batch
+  1 and 8.
 """
 
 from __future__ import annotations
@@ -136,3 +138,15 @@ def test_runner_admission_refusal_exits_2():
     assert rc == 2, (out, err)
     assert out["admitted"] is False and out["admission_reason"] and out["required_bytes"] > 0
     assert "gates" not in out and "tok_s" not in out
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_runner_8b_shapes_pass_their_gates(batch):
+    """The decode-step command at the 32-layer 8B shapes (synthetic weights,
+    4096-position caches): every gate passes, 195 / 259 launches per step."""
+    rc, out, err = run(["--batch", batch, "--steps", 10, "--warmup", 2], timeout=600)
+    assert rc == 0, (out, err)
+    assert out["gates_passed"] is True and all(out["gates"].values())
+    assert out["config"]["n_layers"] == 32 and out["config"]["vocab"] == 128256
+    assert out["launches_per_step"] == (195 if batch == 1 else 259)
+    assert out["tok_s"] > 0
