@@ -102,27 +102,25 @@ __device__ __forceinline__ u32x4 bld_u128(Rsrc r, std::uint32_t voff, std::uint3
 constexpr bool fmt_is_raw_q4k(int f) { return f == RTXLLM_FMT_Q4K_RAW || f == RTXLLM_FMT_Q4K_RAW_PREDECODED; }
 
 // ---- LDS codebooks for the IQ formats ---------------------------------------
-// grid2: IQ2_S index -> eight magnitude bytes 2l+1; grid3: IQ3_S index -> four
-// magnitude bytes; sign: sign byte -> (M_lo, M_hi, E_lo, E_hi), M = 0xFF in the
-// byte of every set bit, E = M & 0x01. A signed int8 weight is (mag ^ M) + E:
-// magnitudes are >= 1, so the per-byte add never carries.
 // Codebooks as read by the bit-exact dequant path.
 static __constant__ std::uint16_t kIq2sGridDev[1024] = {RTXLLM_IQ2S_GRID_VALUES};
 static __constant__ std::uint32_t kIq3sGridDev[512] = {RTXLLM_IQ3S_GRID_VALUES};
 
 // LDS codebooks of the IQ formats. grid2: IQ2_S entry -> its eight magnitude
 // bytes 2 l + 1; grid3: IQ3_S entry -> four magnitude bytes; sign: sign byte ->
-// (M0, M1, E0, E1), where byte j of M is 0xFF and of E is 1 when value j is
-// negative, so a signed int8 word is (magnitude ^ M) + E (no carries: every
-// magnitude is odd).
+// (M0, M1), where byte j of M is 0xFF when value j is negative. Every magnitude
+// is odd, so a signed int8 word is (magnitude ^ M) | 0x01010101 (one v_bitop3):
+// a byte with M = 0 keeps its odd magnitude, and ~mag = -mag - 1 is even, so
+// or-ing in its low bit gives -mag.
 struct IqLds2 {
   uint2 grid2[1024];
-  uint4 sign[256];
+  uint2 sign[256];
 };
 struct IqLds3 {
   std::uint32_t grid3[512];
-  uint4 sign[256];
+  uint2 sign[256];
 };
+constexpr std::uint32_t kIqLowBits = 0x01010101u;
 template <int FMT>
 using IqLds = typename std::conditional<fmt_is_iq2s(FMT), IqLds2, IqLds3>::type;
 
@@ -143,14 +141,12 @@ constexpr void iq_image_signs(IqImage<N>& im, std::size_t at) {
       m0 |= ((i >> j) & 1u) ? (0xFFu << (8 * j)) : 0u;
       m1 |= ((i >> (j + 4)) & 1u) ? (0xFFu << (8 * j)) : 0u;
     }
-    im.w[at + 4 * i] = m0;
-    im.w[at + 4 * i + 1] = m1;
-    im.w[at + 4 * i + 2] = m0 & 0x01010101u;
-    im.w[at + 4 * i + 3] = m1 & 0x01010101u;
+    im.w[at + 2 * i] = m0;
+    im.w[at + 2 * i + 1] = m1;
   }
 }
-constexpr IqImage<3072> iq2s_image() {
-  IqImage<3072> im{};
+constexpr IqImage<2560> iq2s_image() {
+  IqImage<2560> im{};
   for (std::uint32_t i = 0; i < 1024u; ++i) {
     const std::uint32_t w = kIq2sGridSrc[i];
     std::uint32_t lo = 0u, hi = 0u;
@@ -164,15 +160,15 @@ constexpr IqImage<3072> iq2s_image() {
   iq_image_signs(im, 2048);
   return im;
 }
-constexpr IqImage<1536> iq3s_image() {
-  IqImage<1536> im{};
+constexpr IqImage<1024> iq3s_image() {
+  IqImage<1024> im{};
   for (std::uint32_t i = 0; i < 512u; ++i) im.w[i] = kIq3sGridSrc[i];
   iq_image_signs(im, 512);
   return im;
 }
-static_assert(sizeof(IqImage<3072>) == sizeof(IqLds2) && sizeof(IqImage<1536>) == sizeof(IqLds3), "image layout");
-__device__ const IqImage<3072> kIq2sImage = iq2s_image();
-__device__ const IqImage<1536> kIq3sImage = iq3s_image();
+static_assert(sizeof(IqImage<2560>) == sizeof(IqLds2) && sizeof(IqImage<1024>) == sizeof(IqLds3), "image layout");
+__device__ const IqImage<2560> kIq2sImage = iq2s_image();
+__device__ const IqImage<1024> kIq3sImage = iq3s_image();
 
 // The workgroup's codebook copy (only IQ instantiations reference it).
 template <int FMT>
@@ -414,20 +410,20 @@ __device__ __forceinline__ void unit_lookup(const UnitRaw& r, const IqLds<FMT>* 
     for (int grp = 0; grp < 4; ++grp) {
       const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
       const uint2 gm = t->grid2[idx];
-      const uint4 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
-      q.w[2 * grp] = (gm.x ^ sm.x) + sm.z;
-      q.w[2 * grp + 1] = (gm.y ^ sm.y) + sm.w;
+      const uint2 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
+      q.w[2 * grp] = (gm.x ^ sm.x) | kIqLowBits;
+      q.w[2 * grp + 1] = (gm.y ^ sm.y) | kIqLowBits;
     }
   } else {
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
-      const uint4 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
+      const uint2 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
 #pragma unroll
       for (int pair = 0; pair < 2; ++pair) {
         const int sel = 2 * grp + pair;
         const std::uint32_t qb = (r.a[sel >> 2] >> (8 * (sel & 3))) & 0xFFu;
         const std::uint32_t idx = qb | (((r.c[1] >> sel) & 1u) << 8);
-        q.w[sel] = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) + (pair ? sm.w : sm.z);
+        q.w[sel] = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) | kIqLowBits;
       }
     }
   }
