@@ -86,6 +86,17 @@ template <int P>
 __device__ __forceinline__ std::uint32_t bld_u16(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, P);
 }
+// Two 16-bit fields in one register (low, high): the loads write the halves
+// (buffer_load_short_d16 / _d16_hi), so the pair costs one VGPR.
+template <int P>
+__device__ __forceinline__ std::uint32_t bld_u16_pair(Rsrc r, std::uint32_t voff_lo, std::uint32_t soff_lo,
+                                                      std::uint32_t voff_hi, std::uint32_t soff_hi) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 v;
+  v.x = __builtin_amdgcn_raw_buffer_load_b16(r, voff_lo, soff_lo, P);
+  v.y = __builtin_amdgcn_raw_buffer_load_b16(r, voff_hi, soff_hi, P);
+  return __builtin_bit_cast(std::uint32_t, v);
+}
 template <int P>
 __device__ __forceinline__ std::uint32_t bld_u32(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, P);
@@ -294,7 +305,7 @@ __device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k
 struct UnitRaw {
   std::uint32_t a[4];  // K-quants: payload quants; IQ2_S: qs, signs; IQ3_S: qs0, qs1, signs
   std::uint32_t b[4];  // K-quants: native head / metadata
-  std::uint32_t c[4];  // Q5_K: qh bytes; IQ: d, qh, scale byte
+  std::uint32_t c[4];  // Q5_K: qh bytes; IQ: d, qh, scale byte (unit layouts: qh | scale << 8 | d << 16 in c[1])
 };
 
 // Value groups (16-value staging groups) covered by unit k of block b.
@@ -326,13 +337,11 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
     const u32x2 q = bld_u64<P>(rp, u.o[0], 64u * sp);
     r.a[0] = q.x, r.a[1] = q.y;
-    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8, kept in one register
-    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
+    r.c[1] = bld_u16_pair<P>(rp, u.o[1], 16u * sp, u.o[2], 2u * sp);  // qh | scale << 8 | d << 16
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S_UNITS) {
     const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rp, u.o[0], 96u * sp, P);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z;
-    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8
-    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
+    r.c[1] = bld_u16_pair<P>(rp, u.o[1], 16u * sp, u.o[2], 2u * sp);  // qh | scale << 8 | d << 16
   } else if constexpr (fmt_is_iq2s(FMT)) {
     r.c[0] = bld_u16<P>(rp, u.o[0], sp);
     r.a[0] = bld_u32<P>(rp, u.o[1], sp);
@@ -391,8 +400,15 @@ __device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uin
 // own byte in the GGUF layouts. (qh bits above bit 7 never reach an index.)
 template <int FMT>
 __device__ __forceinline__ std::uint32_t iq_scale_byte(const UnitRaw& r) {
-  if constexpr (fmt_is_units(FMT)) return r.c[1] >> 8;
+  if constexpr (fmt_is_units(FMT)) return (r.c[1] >> 8) & 0xFFu;
   else return r.c[2];
+}
+// The IQ block scale d (fp16 bits): the high half of the (qh, scale) register in
+// the unit layouts, its own register in the GGUF layouts.
+template <int FMT>
+__device__ __forceinline__ std::uint32_t iq_d_bits(const UnitRaw& r) {
+  if constexpr (fmt_is_units(FMT)) return r.c[1] >> 16;
+  else return r.c[0];
 }
 
 // IQ units in two phases, so the LDS lookups of one row can be in flight while
@@ -464,7 +480,7 @@ __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, con
       al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
     }
   }
-  const float d = h2f(r.c[0]);
+  const float d = h2f(iq_d_bits<FMT>(r));
   const float D0 = static_cast<float>(dot_digits(ah[0], am[0], al[0]));
   const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   if constexpr (fmt_is_iq2s(FMT)) {
