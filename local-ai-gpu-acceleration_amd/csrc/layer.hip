@@ -28,15 +28,34 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
-// 1 / sqrt(sum / n + eps) from the producer's partial sums of squares. Every
-// lane (and every wave of every kernel) adds the partials in the same order, so
-// all consumers see the same value.
-__device__ __forceinline__ float inv_rms(const float* __restrict__ sumsq, std::uint32_t nslots, std::uint32_t n,
-                                         float eps, std::uint32_t lane) {
-  // lane adds sumsq[lane], sumsq[lane + 64], ... in that order; the loads of
-  // four steps are issued together
+// 1 / sqrt(sum / n + eps) from the producer's partial sums of squares, in two
+// steps so that the matvec's prologue issues its own loads behind these:
+// rms_issue reads the first 256 partials (four per lane, not yet used) and
+// rms_finish adds them, and any further ones, once the prologue has waited for
+// its loads. Every lane (and every wave of every kernel) adds the partials in
+// the same order, sumsq[lane], sumsq[lane + 64], ..., so all consumers see the
+// same value.
+struct RmsPartials {
+  float v[4];
+};
+__device__ __forceinline__ RmsPartials rms_issue(const float* __restrict__ sumsq, std::uint32_t nslots,
+                                                 std::uint32_t lane) {
+  RmsPartials p;
+#pragma unroll
+  for (std::uint32_t j = 0; j < 4u; ++j) {
+    const std::uint32_t i = lane + 64u * j;
+    p.v[j] = sumsq[i < nslots ? i : nslots - 1u];  // masked in rms_finish
+  }
+  return p;
+}
+__device__ __forceinline__ float rms_finish(const RmsPartials& p, const float* __restrict__ sumsq,
+                                            std::uint32_t nslots, std::uint32_t n, float eps, std::uint32_t lane) {
   float s = 0.0f;
-  for (std::uint32_t i0 = lane; i0 < nslots; i0 += 256u) {
+  if (lane < nslots) {
+#pragma unroll
+    for (std::uint32_t j = 0; j < 4u; ++j) s += lane + 64u * j < nslots ? p.v[j] : 0.0f;
+  }
+  for (std::uint32_t i0 = lane + 256u; i0 < nslots; i0 += 256u) {
     float v[4];
 #pragma unroll
     for (std::uint32_t j = 0; j < 4u; ++j) {
@@ -90,10 +109,12 @@ struct EpiQkv {
   KvLayer kv;
   float scale;
   std::uint32_t pos;
+  RmsPartials rp;
   __device__ __forceinline__ void init(std::uint32_t lane) {
-    scale = inv_rms(sumsq, nslots, n, eps, lane);
+    rp = rms_issue(sumsq, nslots, lane);
     pos = *pos_ptr;
   }
+  __device__ __forceinline__ void ready(std::uint32_t lane) { scale = rms_finish(rp, sumsq, nslots, n, eps, lane); }
   __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
     const std::uint32_t row = row0 + (lane >> 4);
     const float y = v * scale;
@@ -125,7 +146,9 @@ struct EpiGateUp {
   float eps;
   float* act;
   float scale;
-  __device__ __forceinline__ void init(std::uint32_t lane) { scale = inv_rms(sumsq, nslots, n, eps, lane); }
+  RmsPartials rp;
+  __device__ __forceinline__ void init(std::uint32_t lane) { rp = rms_issue(sumsq, nslots, lane); }
+  __device__ __forceinline__ void ready(std::uint32_t lane) { scale = rms_finish(rp, sumsq, nslots, n, eps, lane); }
   __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) const {
     const std::uint32_t row = row0 + (lane >> 4);
     const float y = v * scale;
@@ -147,10 +170,12 @@ struct EpiLogits {
   unsigned long long* keys;
   float scale;
   unsigned long long best;
+  RmsPartials rp;
   __device__ __forceinline__ void init(std::uint32_t lane) {
-    scale = inv_rms(sumsq, nslots, n, eps, lane);
+    rp = rms_issue(sumsq, nslots, lane);
     best = 0ull;
   }
+  __device__ __forceinline__ void ready(std::uint32_t lane) { scale = rms_finish(rp, sumsq, nslots, n, eps, lane); }
   __device__ __forceinline__ void operator()(std::uint32_t row0, float v, std::uint32_t lane, std::uint32_t rows) {
     const std::uint32_t row = row0 + (lane >> 4);
     const float y = v * scale;

@@ -20,6 +20,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "iq_grids.h"
@@ -85,17 +86,6 @@ __device__ __forceinline__ std::uint32_t bld_u8(Rsrc r, std::uint32_t voff, std:
 template <int P>
 __device__ __forceinline__ std::uint32_t bld_u16(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, P);
-}
-// Two 16-bit fields in one register (low, high): the loads write the halves
-// (buffer_load_short_d16 / _d16_hi), so the pair costs one VGPR.
-template <int P>
-__device__ __forceinline__ std::uint32_t bld_u16_pair(Rsrc r, std::uint32_t voff_lo, std::uint32_t soff_lo,
-                                                      std::uint32_t voff_hi, std::uint32_t soff_hi) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  u16x2 v;
-  v.x = __builtin_amdgcn_raw_buffer_load_b16(r, voff_lo, soff_lo, P);
-  v.y = __builtin_amdgcn_raw_buffer_load_b16(r, voff_hi, soff_hi, P);
-  return __builtin_bit_cast(std::uint32_t, v);
 }
 template <int P>
 __device__ __forceinline__ std::uint32_t bld_u32(Rsrc r, std::uint32_t voff, std::uint32_t soff) {
@@ -305,7 +295,7 @@ __device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k
 struct UnitRaw {
   std::uint32_t a[4];  // K-quants: payload quants; IQ2_S: qs, signs; IQ3_S: qs0, qs1, signs
   std::uint32_t b[4];  // K-quants: native head / metadata
-  std::uint32_t c[4];  // Q5_K: qh bytes; IQ: d, qh, scale byte (unit layouts: qh | scale << 8 | d << 16 in c[1])
+  std::uint32_t c[4];  // Q5_K: qh bytes; IQ: d, qh, scale byte
 };
 
 // Value groups (16-value staging groups) covered by unit k of block b.
@@ -337,11 +327,13 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
   } else if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
     const u32x2 q = bld_u64<P>(rp, u.o[0], 64u * sp);
     r.a[0] = q.x, r.a[1] = q.y;
-    r.c[1] = bld_u16_pair<P>(rp, u.o[1], 16u * sp, u.o[2], 2u * sp);  // qh | scale << 8 | d << 16
+    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8, kept in one register
+    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S_UNITS) {
     const u32x3 q = __builtin_amdgcn_raw_buffer_load_b96(rp, u.o[0], 96u * sp, P);
     r.a[0] = q.x, r.a[1] = q.y, r.a[2] = q.z;
-    r.c[1] = bld_u16_pair<P>(rp, u.o[1], 16u * sp, u.o[2], 2u * sp);  // qh | scale << 8 | d << 16
+    r.c[1] = bld_u16<P>(rp, u.o[1], 16u * sp);  // qh | scale << 8
+    r.c[0] = bld_u16<P>(rp, u.o[2], 2u * sp);
   } else if constexpr (fmt_is_iq2s(FMT)) {
     r.c[0] = bld_u16<P>(rp, u.o[0], sp);
     r.a[0] = bld_u32<P>(rp, u.o[1], sp);
@@ -400,15 +392,8 @@ __device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uin
 // own byte in the GGUF layouts. (qh bits above bit 7 never reach an index.)
 template <int FMT>
 __device__ __forceinline__ std::uint32_t iq_scale_byte(const UnitRaw& r) {
-  if constexpr (fmt_is_units(FMT)) return (r.c[1] >> 8) & 0xFFu;
+  if constexpr (fmt_is_units(FMT)) return r.c[1] >> 8;
   else return r.c[2];
-}
-// The IQ block scale d (fp16 bits): the high half of the (qh, scale) register in
-// the unit layouts, its own register in the GGUF layouts.
-template <int FMT>
-__device__ __forceinline__ std::uint32_t iq_d_bits(const UnitRaw& r) {
-  if constexpr (fmt_is_units(FMT)) return r.c[1] >> 16;
-  else return r.c[0];
 }
 
 // IQ units in two phases, so the LDS lookups of one row can be in flight while
@@ -480,7 +465,7 @@ __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, con
       al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
     }
   }
-  const float d = h2f(iq_d_bits<FMT>(r));
+  const float d = h2f(r.c[0]);
   const float D0 = static_cast<float>(dot_digits(ah[0], am[0], al[0]));
   const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
   if constexpr (fmt_is_iq2s(FMT)) {
@@ -613,12 +598,6 @@ __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane
 
 constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slots)
 
-// Tile buffers per row group (tiles in flight + 1).
-template <int FMT>
-constexpr int pipe_depth() {
-  return 2;
-}
-
 // Rows per epilogue group: epilogues that declare kGroupRows (a multiple of
 // their tile) receive the results of kGroupRows consecutive rows at once.
 template <class E, class = void>
@@ -628,6 +607,18 @@ struct EpiGroupRows {
 template <class E>
 struct EpiGroupRows<E, std::void_t<decltype(E::kGroupRows)>> {
   static constexpr std::uint32_t value = E::kGroupRows;
+};
+
+// Epilogues with a ready(lane) member get that call once the prologue's loads
+// have been waited for (init(lane) issues their own loads first, ready uses
+// them), so an epilogue's set-up costs no round trip of its own.
+template <class E, class = void>
+struct EpiHasReady {
+  static constexpr bool value = false;
+};
+template <class E>
+struct EpiHasReady<E, std::void_t<decltype(std::declval<E&>().ready(0u))>> {
+  static constexpr bool value = true;
 };
 
 // Epilogues that declare kFinish get epi.finish(slot, lane) from each row
@@ -710,10 +701,14 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     }
   };
 
+  // Loads a tile's rows (clamped to the last row). Called only where the tile
+  // is needed and never inside a branch: the compiler's wait counts then see
+  // one straight sequence per round, so computing tile s waits only for tile
+  // s's loads while tile s + 1's stay in flight (after a conditional load block
+  // it waits for both).
   auto load_tile = [&](std::uint32_t t, UnitRaw (&raw)[TILE][UPL]) {
     // t is wave-uniform; saying so keeps the row bases in SGPRs in every round
     t = __builtin_amdgcn_readfirstlane(t);
-    if (t >= tiles) return;
 #pragma unroll
     for (int rr = 0; rr < TILE; ++rr) {
       std::uint32_t row = t * TILE + rr;
@@ -725,9 +720,9 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   };
 
   // Prologue, ordered so that loads complete in issue order: the epilogue's
-  // set-up (small, waited for at once), the codebook copy into LDS, the staged
-  // activation, then the first tile's weights; the first wait that needs the
-  // codebook leaves the weights in flight.
+  // set-up loads, the codebook copy into LDS, the staged activation, then the
+  // first tile's weights; the first wait (for the codebook, or the epilogue's
+  // set-up) leaves the weights in flight.
   epi.init(lane);
   IqLds<FMT>* tables = nullptr;
   if constexpr (fmt_is_iq(FMT)) {
@@ -752,13 +747,12 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
       xg_load(xs.xq, g1, x1[i]);
     }
   }
-  // A ring of NB tile buffers: tile s + NB - 1 is requested before tile s is
-  // computed, so each row group keeps NB - 1 tiles of weights in flight.
-  constexpr int NB = pipe_depth<FMT>();
-  UnitRaw buf[NB][TILE][UPL];
-#pragma unroll
-  for (int b = 0; b + 1 < NB; ++b) load_tile(tile_of(static_cast<std::uint32_t>(b)), buf[b]);
+  // Two tile buffers: tile s + 1 is requested before tile s is computed, so
+  // each row group keeps one tile of weights in flight.
+  UnitRaw buf[2][TILE][UPL];
+  load_tile(tile_of(0u), buf[0]);
   if constexpr (fmt_is_iq(FMT)) __syncthreads();
+  if constexpr (EpiHasReady<Epi>::value) epi.ready(lane);
   IqLaneScale ls[UPL];
   if constexpr (fmt_is_iq(FMT)) {
 #pragma unroll
@@ -830,15 +824,27 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     }
   };
 
-  for (std::uint32_t s = 0; s < rounds; s += NB) {
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const std::uint32_t sj = s + static_cast<std::uint32_t>(j);
-      if (sj >= rounds) break;  // uniform over the workgroup
-      load_tile(tile_of(sj + NB - 1u), buf[(j + NB - 1) % NB]);
-      finish_tile(tile_of(sj), sj & 1u, (sj >> rshift) & 1u, buf[j]);
-      group_end(sj);
-    }
+  // Round s computes buf[s % 2] after requesting round s + 1 into the other
+  // buffer; the loop runs round pairs while a later round exists, and the last
+  // one or two rounds follow without a request past the end. rounds is uniform
+  // over the workgroup (and >= 1), so are the branches.
+  auto round = [&](std::uint32_t sj, const UnitRaw (&raw)[TILE][UPL]) {
+    finish_tile(tile_of(sj), sj & 1u, (sj >> rshift) & 1u, raw);
+    group_end(sj);
+  };
+  std::uint32_t s = 0;
+  for (; s + 2u < rounds; s += 2u) {
+    load_tile(tile_of(s + 1u), buf[1]);
+    round(s, buf[0]);
+    load_tile(tile_of(s + 2u), buf[0]);
+    round(s + 1u, buf[1]);
+  }
+  if (s + 1u < rounds) {
+    load_tile(tile_of(s + 1u), buf[1]);
+    round(s, buf[0]);
+    round(s + 1u, buf[1]);
+  } else {
+    round(s, buf[0]);
   }
   if constexpr (EpiHasFinish<Epi>::value) {
     if (kw == 0u) epi.finish(blockIdx.x * nrg + rg, lane);
