@@ -828,7 +828,23 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   // buffer; the loop runs round pairs while a later round exists, and the last
   // one or two rounds follow without a request past the end. rounds is uniform
   // over the workgroup (and >= 1), so are the branches.
+  // Wave priority by progress (plain epilogues): a SIMD issues for its oldest
+  // wave first, so with a static tile split the workgroups dispatched first
+  // finish early and the last ones run on at low occupancy. Each round sets the
+  // priority from the fraction of the row group's tiles already done (3 for
+  // the first quarter, ..., 0 for the last), so waves that fell behind are
+  // issued first and the row groups of a CU finish together.
+  const std::uint32_t first = rg * gridDim.x + blockIdx.x;
+  const std::uint32_t active_rounds = first < tiles ? (tiles - first + per_round - 1u) / per_round : 1u;
   auto round = [&](std::uint32_t sj, const UnitRaw (&raw)[TILE][UPL]) {
+    if constexpr (GR == 0u) {
+      switch ((4u * sj) / active_rounds) {
+        case 0: __builtin_amdgcn_s_setprio(3); break;
+        case 1: __builtin_amdgcn_s_setprio(2); break;
+        case 2: __builtin_amdgcn_s_setprio(1); break;
+        default: __builtin_amdgcn_s_setprio(0); break;
+      }
+    }
     finish_tile(tile_of(sj), sj & 1u, (sj >> rshift) & 1u, raw);
     group_end(sj);
   };
