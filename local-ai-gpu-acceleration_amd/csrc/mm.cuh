@@ -322,7 +322,9 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   __shared__ float red[2][kMaxPanels][256];
   const std::uint32_t lane = threadIdx.x & 63u;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const std::uint32_t nw = blockDim.x >> 6;
+  // read once, in an SGPR: a later read of the workgroup size is a vector load,
+  // and its wait would also wait for the ring's loads in flight
+  const std::uint32_t nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
   const std::uint32_t panel = blockIdx.y * nw + wave;  // the launcher makes nw divide the panel count
   const std::uint32_t cols = w.cols, rows = w.rows, bpr = cols >> 8;
   const std::uint32_t q = lane >> 4, r16 = lane & 15u;
@@ -468,7 +470,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
     for (int i = 0; i < 4; ++i) mine[4u * lane + static_cast<std::uint32_t>(i)] = acc[i];
     acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();
-    for (std::uint32_t e = threadIdx.x; e < 256u; e += blockDim.x) {  // whole waves
+    for (std::uint32_t e = threadIdx.x; e < 256u; e += 64u * nw) {  // whole waves
       float v = 0.0f;
       for (std::uint32_t k = 0; k < nw; ++k) v += red[round & 1u][k][e];
       const float tot = v + __shfl_xor(v, 4, 64);  // column n ^ 1 is lane l ^ 1 = element e ^ 4
