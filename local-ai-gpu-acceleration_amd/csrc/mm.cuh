@@ -50,64 +50,48 @@ constexpr bool fmt_mm_supported(int f) {
          f == RTXLLM_FMT_Q4K_SPLIT_NATIVE;
 }
 
-// ---- LDS tables: fp16 codebooks and fp16 sign masks ------------------------------
+// ---- LDS tables: int8 codebooks and sign masks ------------------------------------------
 
-// grid2h: IQ2_S entry -> 8 fp16 magnitudes 2 l + 1; grid3h: IQ3_S entry -> 4
-// fp16 magnitudes; sign16: sign byte -> 8 x 0x8000 / 0 masks.
+// grid2b: IQ2_S entry -> its 8 magnitude bytes 2 l + 1, each ^ 0x80; grid3b: IQ3_S
+// entry -> 4 magnitude bytes ^ 0x80; sign: sign byte -> (M0, M1), byte j of M
+// 0xFF when value j is negative. As in the batch-1 decode, (g ^ M) | 0x01010101
+// signs the odd magnitudes in one v_bitop3; with the stored ^ 0x80 each byte
+// comes out as 128 + w, the biased form mm_biased_pair turns into fp16.
 struct MmLds2 {
-  uint4 grid2h[1024];
-  uint4 sign16[256];
+  uint2 grid2b[1024];
+  uint2 sign[256];
 };
 struct MmLds3 {
-  uint2 grid3h[512];
-  uint4 sign16[256];
+  std::uint32_t grid3b[512];
+  uint2 sign[256];
 };
 template <int FMT>
 using MmLds = typename std::conditional<FMT == RTXLLM_FMT_IQ2S, MmLds2, MmLds3>::type;
 
-constexpr std::uint16_t f16_of_small(std::uint32_t v) {  // exact fp16 bits of an integer 1..2047
-  std::uint32_t e = 0;
-  while ((v >> (e + 1)) != 0u) ++e;
-  const std::uint32_t mant = (v << (10 - e)) & 0x3FFu;
-  return static_cast<std::uint16_t>(((e + 15u) << 10) | mant);
-}
-
-template <std::size_t N>
-constexpr void mm_image_signs(IqImage<N>& im, std::size_t at) {
-  for (std::uint32_t i = 0; i < 256u; ++i)
-    for (std::uint32_t j = 0; j < 4u; ++j) {
-      const std::uint32_t lo = ((i >> (2 * j)) & 1u) ? 0x8000u : 0u;
-      const std::uint32_t hi = ((i >> (2 * j + 1)) & 1u) ? 0x8000u : 0u;
-      im.w[at + 4 * i + j] = lo | (hi << 16);
+constexpr IqImage<2560> mm2_image() {
+  IqImage<2560> im{};
+  for (std::uint32_t i = 0; i < 1024u; ++i) {
+    const std::uint32_t w = kIq2sGridSrc[i];
+    std::uint32_t lo = 0u, hi = 0u;
+    for (int j = 0; j < 4; ++j) {
+      lo |= ((2u * ((w >> (2 * j)) & 3u) + 1u) ^ 0x80u) << (8 * j);
+      hi |= ((2u * ((w >> (2 * j + 8)) & 3u) + 1u) ^ 0x80u) << (8 * j);
     }
-}
-constexpr IqImage<5120> mm2_image() {
-  IqImage<5120> im{};
-  for (std::uint32_t i = 0; i < 1024u; ++i)
-    for (std::uint32_t j = 0; j < 4u; ++j) {
-      const std::uint32_t w = kIq2sGridSrc[i];
-      const std::uint32_t lo = f16_of_small(2u * ((w >> (4 * j)) & 3u) + 1u);
-      const std::uint32_t hi = f16_of_small(2u * ((w >> (4 * j + 2)) & 3u) + 1u);
-      im.w[4 * i + j] = lo | (hi << 16);
-    }
-  mm_image_signs(im, 4096);
+    im.w[2 * i] = lo;
+    im.w[2 * i + 1] = hi;
+  }
+  iq_image_signs(im, 2048);
   return im;
 }
-constexpr IqImage<2048> mm3_image() {
-  IqImage<2048> im{};
-  for (std::uint32_t i = 0; i < 512u; ++i)
-    for (std::uint32_t j = 0; j < 2u; ++j) {
-      const std::uint32_t w = kIq3sGridSrc[i];
-      const std::uint32_t lo = f16_of_small((w >> (16 * j)) & 0xFFu);
-      const std::uint32_t hi = f16_of_small((w >> (16 * j + 8)) & 0xFFu);
-      im.w[2 * i + j] = lo | (hi << 16);
-    }
-  mm_image_signs(im, 1024);
+constexpr IqImage<1024> mm3_image() {
+  IqImage<1024> im{};
+  for (std::uint32_t i = 0; i < 512u; ++i) im.w[i] = kIq3sGridSrc[i] ^ 0x80808080u;
+  iq_image_signs(im, 512);
   return im;
 }
-static_assert(sizeof(IqImage<5120>) == sizeof(MmLds2) && sizeof(IqImage<2048>) == sizeof(MmLds3), "mm images");
-__device__ const IqImage<5120> kMm2Image = mm2_image();
-__device__ const IqImage<2048> kMm3Image = mm3_image();
+static_assert(sizeof(IqImage<2560>) == sizeof(MmLds2) && sizeof(IqImage<1024>) == sizeof(MmLds3), "mm images");
+__device__ const IqImage<2560> kMm2Image = mm2_image();
+__device__ const IqImage<1024> kMm3Image = mm3_image();
 
 template <int FMT>
 __device__ __forceinline__ MmLds<FMT>& mm_lds() {
@@ -201,6 +185,18 @@ __device__ __forceinline__ std::uint32_t small_pair_times(std::uint32_t fields, 
   return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_fma(v, mm, c));
 }
 
+// Two fp16 products w m from bytes b0, b1 of `biased` (selector 0x04010400) or
+// b2, b3 (0x04030402), each byte 128 + w: the halves (0x64 << 8 | byte) are
+// 1152 + w, and fma(1152 + w, m, -1152 m) = w m in one rounding (exact: |w m|
+// < 2048, and 1152 m = 2^7 * 9 m is an fp16 integer for m < 228).
+__device__ __forceinline__ std::uint32_t mm_biased_pair(std::uint32_t biased, std::uint32_t sel, _Float16 m) {
+  typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+  const half2 v = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, biased, sel));
+  const half2 mm = {m, m};
+  const half2 c = {static_cast<_Float16>(-1152.0f) * m, static_cast<_Float16>(-1152.0f) * m};
+  return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_fma(v, mm, c));
+}
+
 // A operand of instruction j (values 64 q + 8 j .. + 8 of the block).
 template <int FMT>
 __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, int j, std::uint32_t q,
@@ -210,12 +206,13 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
     const std::uint32_t qh = (std::uint32_t{r.s[1]} >> (8 * (j >> 2))) & 0xFFu;  // qh of sub-block 2 q + j / 4
     const std::uint32_t idx = qsb | (((qh >> (2 * (j & 3))) & 3u) << 8);
     const std::uint32_t sgb = (r.a[2 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
-    const uint4 g = t->grid2h[idx];
-    const uint4 sm = t->sign16[sgb];
+    const uint2 g = t->grid2b[idx];
+    const uint2 sm = t->sign[sgb];
     const std::uint32_t nib = ((std::uint32_t{r.s[2]} >> (8 * (j >> 2))) >> (4 * ((j & 3) >> 1))) & 15u;
     const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
-    const half8 a = as_half8(make_uint4(g.x ^ sm.x, g.y ^ sm.y, g.z ^ sm.z, g.w ^ sm.w));
-    return a * m;
+    const std::uint32_t b0 = (g.x ^ sm.x) | 0x01010101u, b1 = (g.y ^ sm.y) | 0x01010101u;
+    return as_half8(make_uint4(mm_biased_pair(b0, 0x04010400u, m), mm_biased_pair(b0, 0x04030402u, m),
+                               mm_biased_pair(b1, 0x04010400u, m), mm_biased_pair(b1, 0x04030402u, m)));
   } else if constexpr (FMT == RTXLLM_FMT_IQ3S) {
     const std::uint32_t sub = static_cast<std::uint32_t>(j >> 2);          // 32-value sub-block 2 q + sub
     const std::uint32_t qh = (std::uint32_t{r.s[1]} >> (8 * sub)) & 0xFFu;
@@ -224,12 +221,13 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
     const std::uint32_t i0 = (w16 & 0xFFu) | (((qh >> sel0) & 1u) << 8);
     const std::uint32_t i1 = ((w16 >> 8) & 0xFFu) | (((qh >> sel1) & 1u) << 8);
     const std::uint32_t sgb = (r.a[4 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
-    const uint2 g0 = t->grid3h[i0], g1 = t->grid3h[i1];
-    const uint4 sm = t->sign16[sgb];
+    const std::uint32_t g0 = t->grid3b[i0], g1 = t->grid3b[i1];
+    const uint2 sm = t->sign[sgb];
     const std::uint32_t nib = (std::uint32_t{r.s8} >> (4u * sub)) & 15u;
     const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
-    const half8 a = as_half8(make_uint4(g0.x ^ sm.x, g0.y ^ sm.y, g1.x ^ sm.z, g1.y ^ sm.w));
-    return a * m;
+    const std::uint32_t b0 = (g0 ^ sm.x) | 0x01010101u, b1 = (g1 ^ sm.y) | 0x01010101u;
+    return as_half8(make_uint4(mm_biased_pair(b0, 0x04010400u, m), mm_biased_pair(b0, 0x04030402u, m),
+                               mm_biased_pair(b1, 0x04010400u, m), mm_biased_pair(b1, 0x04030402u, m)));
   } else {
     // K-quants: j < 4 low nibbles of bytes 8 j .. + 8 of the lane's 32 (sub-block
     // 2 q), j >= 4 high nibbles of bytes 8 (j - 4) .. (sub-block 2 q + 1).
