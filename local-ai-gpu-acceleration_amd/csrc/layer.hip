@@ -30,7 +30,8 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 
 // 1 / sqrt(sum / n + eps) from the producer's partial sums of squares, in two
 // steps so that the matvec's prologue issues its own loads behind these:
-// rms_issue reads the first 256 partials (four per lane, not yet used) and
+// rms_issue reads the first 256 partials (four per lane, not yet used; the
+// launchers refuse nslots = 0, so the clamped index stays in the array) and
 // rms_finish adds them, and any further ones, once the prologue has waited for
 // its loads. Every lane (and every wave of every kernel) adds the partials in
 // the same order, sumsq[lane], sumsq[lane + 64], ..., so all consumers see the
@@ -661,7 +662,7 @@ hipError_t launch_qkv(int fmt, const std::uint8_t* payload, const std::uint8_t* 
                       const NormIn& in, std::uint32_t q_rows, std::uint32_t kv_rows, const float2* rope,
                       std::uint32_t rope_positions, const std::uint32_t* pos, void* q_out, const KvLayer& kv,
                       hipStream_t stream) {
-  if (rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || kv.page_size == 0u ||
+  if (rope == nullptr || rope_positions == 0u || kv.n_kv == 0u || kv.page_size == 0u || in.nslots == 0u ||
       q_rows % (kHeadDim * kv.n_kv) != 0u)
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, q_rows + 2u * kv_rows, cols};
@@ -740,7 +741,7 @@ hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint
 
 hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
                           std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream) {
-  if ((rows % 4u) != 0u) return hipErrorInvalidValue;
+  if ((rows % 4u) != 0u || in.nslots == 0u) return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   EpiGateUp e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.act = act;
@@ -757,7 +758,7 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
                          std::uint32_t cols, const NormIn& in, float* logits, unsigned long long* keys,
                          std::uint32_t key_capacity, std::uint32_t* key_count, hipStream_t stream) {
   const std::uint32_t slots = logits_key_slots(fmt, rows, cols);
-  if (slots == 0u || slots > key_capacity || keys == nullptr) return hipErrorInvalidValue;
+  if (slots == 0u || slots > key_capacity || keys == nullptr || in.nslots == 0u) return hipErrorInvalidValue;
   if (key_count != nullptr) *key_count = slots;
   const QTensor w{payload, meta, rows, cols};
   EpiLogits e{};
