@@ -407,23 +407,35 @@ struct IqWords {
 template <int FMT>
 __device__ __forceinline__ void unit_lookup(const UnitRaw& r, const IqLds<FMT>* t, IqWords& q) {
   if constexpr (fmt_is_iq2s(FMT)) {
+    // the high index bits of group g, (qh >> 2 g) & 3, one per byte of hb:
+    // qh | qh << 6 | qh << 12 | qh << 18 puts them at bits 8 g (ors, no carries)
+    const std::uint32_t qh = r.c[1] & 0xFFu;
+    const std::uint32_t s6 = (qh << 6) | qh;
+    const std::uint32_t hb = ((s6 << 12) | s6) & 0x03030303u;
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
-      const std::uint32_t idx = ((r.a[0] >> (8 * grp)) & 0xFFu) | ((r.c[1] << (8 - 2 * grp)) & 0x300u);
+      // index = qs byte | high bits << 8: bytes grp of (qs, hb) into bytes 0, 1
+      const std::uint32_t idx = __builtin_amdgcn_perm(hb, r.a[0], 0x0C0C0400u + 0x101u * static_cast<std::uint32_t>(grp));
       const uint2 gm = t->grid2[idx];
       const uint2 sm = t->sign[(r.a[1] >> (8 * grp)) & 0xFFu];
       q.w[2 * grp] = (gm.x ^ sm.x) | kIqLowBits;
       q.w[2 * grp + 1] = (gm.y ^ sm.y) | kIqLowBits;
     }
   } else {
+    // the high index bit of value group j, (qh >> j) & 1, one per byte of
+    // (hb0: j < 4, hb1: j >= 4): qh | qh << 7 | qh << 14 | qh << 21 (ors)
+    const std::uint32_t qh = r.c[1] & 0xFFu;
+    const std::uint32_t s7 = (qh << 7) | qh;
+    const std::uint32_t s14 = (s7 << 14) | s7;
+    const std::uint32_t hb0 = s14 & 0x01010101u, hb1 = (s14 >> 4) & 0x01010101u;
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const uint2 sm = t->sign[(r.a[2] >> (8 * grp)) & 0xFFu];
 #pragma unroll
       for (int pair = 0; pair < 2; ++pair) {
         const int sel = 2 * grp + pair;
-        const std::uint32_t qb = (r.a[sel >> 2] >> (8 * (sel & 3))) & 0xFFu;
-        const std::uint32_t idx = qb | (((r.c[1] >> sel) & 1u) << 8);
+        const std::uint32_t idx = __builtin_amdgcn_perm(sel < 4 ? hb0 : hb1, r.a[sel >> 2],
+                                                        0x0C0C0400u + 0x101u * static_cast<std::uint32_t>(sel & 3));
         q.w[sel] = (t->grid3[idx] ^ (pair ? sm.y : sm.x)) | kIqLowBits;
       }
     }
