@@ -462,24 +462,9 @@ __device__ __forceinline__ IqLaneScale iq_lane_scale(std::uint32_t k, const XG& 
 template <int FMT>
 __device__ __forceinline__ float unit_dot_iq(const UnitRaw& r, const XG& x0, const XG& x1, const IqLaneScale& ls,
                                              const IqWords& q) {
-  int ah[2], am[2], al[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const XG& xg = s ? x1 : x0;
-    ah[s] = sdot4_0(q.w[4 * s], xg.h[0]);
-    am[s] = sdot4_0(q.w[4 * s], xg.m[0]);
-    al[s] = sdot4_0(q.w[4 * s], xg.l[0]);
-#pragma unroll
-    for (int o = 1; o < 4; ++o) {
-      const int w = static_cast<int>(q.w[4 * s + o]);
-      ah[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.h[o]), ah[s], false);
-      am[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.m[o]), am[s], false);
-      al[s] = __builtin_amdgcn_sdot4(w, static_cast<int>(xg.l[o]), al[s], false);
-    }
-  }
   const float d = h2f(r.c[0]);
-  const float D0 = static_cast<float>(dot_digits(ah[0], am[0], al[0]));
-  const float D1 = static_cast<float>(dot_digits(ah[1], am[1], al[1]));
+  const float D0 = static_cast<float>(dot16(q.w, x0));
+  const float D1 = static_cast<float>(dot16(q.w + 4, x1));
   if constexpr (fmt_is_iq2s(FMT)) {
     // d * (0.5 + n) / 4 * s = d * (n * s / 4 + s / 8)
     const std::uint32_t sc = iq_scale_byte<FMT>(r);

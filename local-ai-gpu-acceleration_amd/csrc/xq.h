@@ -197,33 +197,26 @@ __device__ __forceinline__ void xg_store(const XQOut& x, std::uint32_t group, co
   x.sum[group] = g.sum;
 }
 
-// sum_j w_j X_j = 65536 sum w H + 256 sum w M + sum w L over a 16-value group:
-// exact in int32 for weight codes |w| <= 31 (|result| <= 16 * 31 * 2^22 <
-// 2^31), so the two shift-adds may wrap in between without changing it.
-__device__ __forceinline__ int dot_digits(int ah, int am, int al) {
-  const std::uint32_t lo = (static_cast<std::uint32_t>(am) << 8) + static_cast<std::uint32_t>(al);
-  return static_cast<int>((static_cast<std::uint32_t>(ah) << 16) + lo);
-}
-
-// a . b over four int8 lanes, starting a chain from 0: the three-operand
-// encoding with an inline zero accumulator (the two-operand accumulate form
-// would need the zero moved into its destination first).
-__device__ __forceinline__ int sdot4_0(std::uint32_t a, std::uint32_t b) {
-  int r;
-  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
-// The dot of 16 int8 weights (4 words) with a staged group.
+// The dot of 16 int8 weights (4 words) with a staged group: sum_j w_j X_j =
+// 65536 sum w H + 256 sum w M + sum w L, exact in int32 for weight codes |w| <=
+// 31 (|result| <= 16 * 31 * 2^22 < 2^31). One chain of dot4 accumulations:
+// the H sums from 0, then the M sums from that shifted by 8, then the L sums
+// from that shifted by 8, i.e. ((sum w H) 256 + sum w M) 256 + sum w L; the
+// shifts and adds may wrap in between without changing the result. All of it
+// goes through the builtin, so the compiler sees each dot instruction (a
+// dot's result read by a different VALU opcode needs three wait states,
+// which its hazard pass inserts only for instructions it can see).
 __device__ __forceinline__ int dot16(const std::uint32_t w[4], const XG& x) {
-  int ah = sdot4_0(w[0], x.h[0]), am = sdot4_0(w[0], x.m[0]), al = sdot4_0(w[0], x.l[0]);
+  int a = __builtin_amdgcn_sdot4(static_cast<int>(w[0]), static_cast<int>(x.h[0]), 0, false);
 #pragma unroll
-  for (int i = 1; i < 4; ++i) {
-    ah = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.h[i]), ah, false);
-    am = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.m[i]), am, false);
-    al = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.l[i]), al, false);
-  }
-  return dot_digits(ah, am, al);
+  for (int i = 1; i < 4; ++i) a = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.h[i]), a, false);
+  a = static_cast<int>(static_cast<std::uint32_t>(a) << 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.m[i]), a, false);
+  a = static_cast<int>(static_cast<std::uint32_t>(a) << 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), static_cast<int>(x.l[i]), a, false);
+  return a;
 }
 
 }  // namespace rtxllm
