@@ -126,7 +126,8 @@ template <int FMT>
 using IqLds = typename std::conditional<fmt_is_iq2s(FMT), IqLds2, IqLds3>::type;
 
 // The same tables as device-global images, built at compile time, in the LDS
-// layout: a workgroup copies its image with direct global -> LDS loads.
+// layout: a workgroup copies the grid part with direct global -> LDS loads and
+// computes the sign part (iq_sign_mask, checked against the image below).
 template <std::size_t N>
 struct IqImage {
   std::uint32_t w[N];
@@ -168,6 +169,21 @@ constexpr IqImage<1024> iq3s_image() {
   return im;
 }
 static_assert(sizeof(IqImage<2560>) == sizeof(IqLds2) && sizeof(IqImage<1024>) == sizeof(IqLds3), "image layout");
+
+// Sign mask of a nibble n: bit j of n spread to bit 8 j by two shift-ors (no
+// two copies of n meet in a kept bit), masked, times 0xFF.
+constexpr std::uint32_t iq_sign_mask(std::uint32_t n) {
+  const std::uint32_t t7 = n | (n << 7);
+  const std::uint32_t b = (t7 | (t7 << 14)) & 0x01010101u;
+  return (b << 8) - b;
+}
+constexpr bool iq_sign_masks_match() {
+  const IqImage<1024> im = iq3s_image();
+  for (std::uint32_t i = 0; i < 256u; ++i)
+    if (im.w[512 + 2 * i] != iq_sign_mask(i & 15u) || im.w[512 + 2 * i + 1] != iq_sign_mask(i >> 4)) return false;
+  return true;
+}
+static_assert(iq_sign_masks_match(), "computed sign table");
 __device__ const IqImage<2560> kIq2sImage = iq2s_image();
 __device__ const IqImage<1024> kIq3sImage = iq3s_image();
 
@@ -178,13 +194,16 @@ __device__ __forceinline__ IqLds<FMT>& iq_lds() {
   return t;
 }
 
-// Start the copy of the codebook image into LDS: 16 B per lane, 1 KB per wave
-// instruction, spread over the workgroup's waves. Asynchronous: the caller
-// waits (s_waitcnt + barrier) before the first lookup.
+// Fill the workgroup's codebook: the grid part of the image is copied with
+// direct global -> LDS loads (16 B per lane, 1 KB per wave instruction, spread
+// over the workgroup's waves; asynchronous: the caller waits with s_waitcnt +
+// barrier before the first lookup), and the sign table is computed, which
+// keeps 2 KB per workgroup off the L2 at the kernel's start.
 template <int FMT>
 __device__ __forceinline__ void iq_lds_fetch(IqLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
-  constexpr std::uint32_t kChunks = sizeof(IqLds<FMT>) / 1024u;  // 1 KB per wave instruction
-  static_assert(sizeof(IqLds<FMT>) % 1024u == 0u, "whole wave chunks");
+  constexpr std::uint32_t kGridBytes = sizeof(IqLds<FMT>) - sizeof(t.sign);
+  constexpr std::uint32_t kChunks = kGridBytes / 1024u;
+  static_assert(kGridBytes % 1024u == 0u, "whole wave chunks");
   const std::uint32_t nw = blockDim.x >> 6;
   const uint4* src = reinterpret_cast<const uint4*>(fmt_is_iq2s(FMT) ? static_cast<const void*>(&kIq2sImage)
                                                                       : static_cast<const void*>(&kIq3sImage));
@@ -192,6 +211,8 @@ __device__ __forceinline__ void iq_lds_fetch(IqLds<FMT>& t, std::uint32_t wave, 
   for (std::uint32_t c = wave; c < kChunks; c += nw)
     __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
                                      (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
+  for (std::uint32_t e = 64u * wave + lane; e < 256u; e += 64u * nw)
+    t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
 }
 
 // ---- per-format unit load + compute ------------------------------------------
