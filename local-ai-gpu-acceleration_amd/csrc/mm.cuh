@@ -99,10 +99,13 @@ __device__ __forceinline__ MmLds<FMT>& mm_lds() {
   return t;
 }
 
+// The grid part is copied (direct global -> LDS loads), the sign table computed
+// (the batch-1 codebook's rule, iq_sign_mask).
 template <int FMT>
 __device__ __forceinline__ void mm_lds_fetch(MmLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
-  constexpr std::uint32_t kChunks = sizeof(MmLds<FMT>) / 1024u;
-  static_assert(sizeof(MmLds<FMT>) % 1024u == 0u, "whole wave chunks");
+  constexpr std::uint32_t kGridBytes = sizeof(MmLds<FMT>) - sizeof(t.sign);
+  constexpr std::uint32_t kChunks = kGridBytes / 1024u;
+  static_assert(kGridBytes % 1024u == 0u, "whole wave chunks");
   const std::uint32_t nw = blockDim.x >> 6;
   const uint4* src = reinterpret_cast<const uint4*>(FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kMm2Image)
                                                                            : static_cast<const void*>(&kMm3Image));
@@ -110,6 +113,8 @@ __device__ __forceinline__ void mm_lds_fetch(MmLds<FMT>& t, std::uint32_t wave, 
   for (std::uint32_t c = wave; c < kChunks; c += nw)
     __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
                                      (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
+  for (std::uint32_t e = 64u * wave + lane; e < 256u; e += 64u * nw)
+    t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
 }
 
 // ---- per-lane block fields --------------------------------------------------------
