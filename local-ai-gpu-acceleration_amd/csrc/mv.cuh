@@ -194,25 +194,59 @@ __device__ __forceinline__ IqLds<FMT>& iq_lds() {
   return t;
 }
 
-// Fill the workgroup's codebook: the grid part of the image is copied with
-// direct global -> LDS loads (16 B per lane, 1 KB per wave instruction, spread
-// over the workgroup's waves; asynchronous: the caller waits with s_waitcnt +
-// barrier before the first lookup), and the sign table is computed, which
-// keeps 2 KB per workgroup off the L2 at the kernel's start.
+// Filling the workgroup's codebook, in two steps around the rest of the
+// prologue's loads (workgroups of at least two waves, which the launch
+// geometry guarantees for the IQ formats):
+//  * iq_grid_issue loads the grid part of the image into registers, 16 B per
+//    thread per step, first among the wave's loads (a thread whose step falls
+//    past the grid re-reads the last piece);
+//  * iq_lds_commit, after the activation and first-tile loads are issued,
+//    writes the pieces to LDS, computes the sign table (which keeps 2 KB per
+//    workgroup off the L2), waits for its LDS writes and meets the
+//    workgroup's other waves at the barrier.
+// The compiler counts these plain loads exactly, so the writes wait for the
+// grid loads only: the activation and the first tile stay in flight through
+// the barrier, and the first round requests the next tile before they
+// arrive. A __syncthreads() (a workgroup fence) would wait for all of them,
+// and so would a read after a direct-to-LDS copy (the compiler waits for
+// every outstanding load there). The empty asm statements keep LDS accesses
+// on their side of the bare s_barrier.
 template <int FMT>
-__device__ __forceinline__ void iq_lds_fetch(IqLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
-  constexpr std::uint32_t kGridBytes = sizeof(IqLds<FMT>) - sizeof(t.sign);
-  constexpr std::uint32_t kChunks = kGridBytes / 1024u;
-  static_assert(kGridBytes % 1024u == 0u, "whole wave chunks");
-  const std::uint32_t nw = blockDim.x >> 6;
+struct IqGridStage {
+  static constexpr std::uint32_t kUnits = (sizeof(IqLds<FMT>) - 256u * sizeof(uint2)) / 16u;  // 16-byte pieces
+  static constexpr std::uint32_t kPer = (kUnits + 127u) / 128u;  // per thread with two or more waves
+  uint4 v[kPer];
+};
+template <int FMT>
+__device__ __forceinline__ void iq_grid_issue(IqGridStage<FMT>& g, std::uint32_t tid, std::uint32_t nt) {
+  constexpr std::uint32_t U = IqGridStage<FMT>::kUnits;
   const uint4* src = reinterpret_cast<const uint4*>(fmt_is_iq2s(FMT) ? static_cast<const void*>(&kIq2sImage)
                                                                       : static_cast<const void*>(&kIq3sImage));
+#pragma unroll
+  for (std::uint32_t j = 0; j < IqGridStage<FMT>::kPer; ++j) {
+    const std::uint32_t c = tid + j * nt;
+    g.v[j] = src[c < U ? c : U - 1u];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // issued here, ahead of the later loads (not next to their writes)
+}
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt left alone
+template <int FMT>
+__device__ __forceinline__ void iq_lds_commit(IqLds<FMT>& t, const IqGridStage<FMT>& g, std::uint32_t tid,
+                                              std::uint32_t nt) {
+  constexpr std::uint32_t U = IqGridStage<FMT>::kUnits;
   uint4* dst = reinterpret_cast<uint4*>(&t);
-  for (std::uint32_t c = wave; c < kChunks; c += nw)
-    __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
-                                     (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
-  for (std::uint32_t e = 64u * wave + lane; e < 256u; e += 64u * nw)
-    t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
+#pragma unroll
+  for (std::uint32_t j = 0; j < IqGridStage<FMT>::kPer; ++j) {
+    // no branch (the load would move into it): a re-read last piece is
+    // stored again, the same bytes to the same place
+    const std::uint32_t c = tid + j * nt;
+    dst[c < U ? c : U - 1u] = g.v[j];
+  }
+  for (std::uint32_t e = tid; e < 256u; e += nt) t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ---- per-format unit load + compute ------------------------------------------
@@ -738,14 +772,15 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   };
 
   // Prologue, ordered so that loads complete in issue order: the epilogue's
-  // set-up loads, the codebook copy into LDS, the staged activation, then the
-  // first tile's weights; the first wait (for the codebook, or the epilogue's
-  // set-up) leaves the weights in flight.
+  // set-up loads, the codebook grid (into registers), the staged activation,
+  // then the first tile's weights; the codebook commit waits for the grid
+  // loads only and leaves the activation and the weights in flight.
   epi.init(lane);
   IqLds<FMT>* tables = nullptr;
+  IqGridStage<FMT> grid_stage;
   if constexpr (fmt_is_iq(FMT)) {
     tables = &iq_lds<FMT>();
-    iq_lds_fetch<FMT>(*tables, wave, lane);
+    iq_grid_issue<FMT>(grid_stage, threadIdx.x, blockDim.x);
   }
   XG x0[UPL], x1[UPL];
 #pragma unroll
@@ -769,7 +804,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   // each row group keeps one tile of weights in flight.
   UnitRaw buf[2][TILE][UPL];
   load_tile(tile_of(0u), buf[0]);
-  if constexpr (fmt_is_iq(FMT)) __syncthreads();
+  if constexpr (fmt_is_iq(FMT)) iq_lds_commit<FMT>(*tables, grid_stage, threadIdx.x, blockDim.x);
   if constexpr (EpiHasReady<Epi>::value) epi.ready(lane);
   IqLaneScale ls[UPL];
   if constexpr (fmt_is_iq(FMT)) {
