@@ -99,22 +99,13 @@ __device__ __forceinline__ MmLds<FMT>& mm_lds() {
   return t;
 }
 
-// The grid part is copied (direct global -> LDS loads), the sign table computed
-// (the batch-1 codebook's rule, iq_sign_mask).
+// The codebook fill of the batch kernels: lds_grid_issue / lds_grid_commit,
+// sized for workgroups of eight waves (one 16-byte piece per thread).
 template <int FMT>
-__device__ __forceinline__ void mm_lds_fetch(MmLds<FMT>& t, std::uint32_t wave, std::uint32_t lane) {
-  constexpr std::uint32_t kGridBytes = sizeof(MmLds<FMT>) - sizeof(t.sign);
-  constexpr std::uint32_t kChunks = kGridBytes / 1024u;
-  static_assert(kGridBytes % 1024u == 0u, "whole wave chunks");
-  const std::uint32_t nw = blockDim.x >> 6;
-  const uint4* src = reinterpret_cast<const uint4*>(FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kMm2Image)
-                                                                           : static_cast<const void*>(&kMm3Image));
-  uint4* dst = reinterpret_cast<uint4*>(&t);
-  for (std::uint32_t c = wave; c < kChunks; c += nw)
-    __builtin_amdgcn_global_load_lds(src + 64u * c + lane,
-                                     (__attribute__((address_space(3))) void*)(dst + 64u * c), 16, 0, 0);
-  for (std::uint32_t e = 64u * wave + lane; e < 256u; e += 64u * nw)
-    t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
+using MmGridStage = LdsGridStage<MmLds<FMT>, 512u>;
+template <int FMT>
+__device__ __forceinline__ const void* mm_image() {
+  return FMT == RTXLLM_FMT_IQ2S ? static_cast<const void*>(&kMm2Image) : static_cast<const void*>(&kMm3Image);
 }
 
 // ---- per-lane block fields --------------------------------------------------------
@@ -411,10 +402,10 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const Rsrc rsm = make_rsrc(FmtBytes<FMT>::meta > 0u ? w.meta : w.payload, rows * mrow);
 
   const MmLds<FMT>* tables = nullptr;
+  MmGridStage<FMT> grid_stage;
   if constexpr (fmt_is_iq(FMT)) {
-    MmLds<FMT>& t = mm_lds<FMT>();
-    mm_lds_fetch<FMT>(t, wave, lane);
-    tables = &t;
+    tables = &mm_lds<FMT>();
+    lds_grid_issue(grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
   }
 
   // (tile, block) units of this wave in order: unit u -> tile blockIdx.x +
@@ -439,7 +430,8 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   MmRaw ring[NB];
 #pragma unroll
   for (int j = 0; j < NB - 1; ++j) load_unit(static_cast<std::uint32_t>(j), ring[j]);
-  if constexpr (fmt_is_iq(FMT)) __syncthreads();
+  if constexpr (fmt_is_iq(FMT))
+    lds_grid_commit(mm_lds<FMT>(), grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
 
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto finish_unit = [&](std::uint32_t u, const MmRaw& raw) {

@@ -194,59 +194,67 @@ __device__ __forceinline__ IqLds<FMT>& iq_lds() {
   return t;
 }
 
-// Filling the workgroup's codebook, in two steps around the rest of the
-// prologue's loads (workgroups of at least two waves, which the launch
-// geometry guarantees for the IQ formats):
-//  * iq_grid_issue loads the grid part of the image into registers, 16 B per
-//    thread per step, first among the wave's loads (a thread whose step falls
-//    past the grid re-reads the last piece);
-//  * iq_lds_commit, after the activation and first-tile loads are issued,
-//    writes the pieces to LDS, computes the sign table (which keeps 2 KB per
-//    workgroup off the L2), waits for its LDS writes and meets the
-//    workgroup's other waves at the barrier.
+// Filling a workgroup's codebook table T (a grid part, then sign[256]), in two
+// steps around the rest of the prologue's loads:
+//  * lds_grid_issue loads the grid part of the image into registers, 16 B per
+//    thread per step for NT threads (a thread whose step falls past the grid
+//    re-reads the last piece), first among the wave's loads;
+//  * lds_grid_commit, after the activation and first-tile loads are issued,
+//    writes the pieces to LDS (smaller workgroups add the rest piece by
+//    piece), computes the sign table (which keeps 2 KB per workgroup off the
+//    L2), waits for its LDS writes and meets the workgroup's other waves at the
+//    barrier.
 // The compiler counts these plain loads exactly, so the writes wait for the
 // grid loads only: the activation and the first tile stay in flight through
-// the barrier, and the first round requests the next tile before they
-// arrive. A __syncthreads() (a workgroup fence) would wait for all of them,
-// and so would a read after a direct-to-LDS copy (the compiler waits for
-// every outstanding load there). The empty asm statements keep LDS accesses
-// on their side of the bare s_barrier.
-template <int FMT>
-struct IqGridStage {
-  static constexpr std::uint32_t kUnits = (sizeof(IqLds<FMT>) - 256u * sizeof(uint2)) / 16u;  // 16-byte pieces
-  static constexpr std::uint32_t kPer = (kUnits + 127u) / 128u;  // per thread with two or more waves
+// the barrier, and the first round starts on the rows that have arrived. A
+// __syncthreads() (a workgroup fence) would wait for all of them, and so would
+// a read after a direct-to-LDS copy (the compiler waits for every outstanding
+// load there). The writes carry no branch (a load would move into it): a
+// re-read last piece is stored again, the same bytes to the same place. The
+// empty asm statements keep LDS accesses on their side of the bare s_barrier.
+template <class T, std::uint32_t NT>
+struct LdsGridStage {
+  static constexpr std::uint32_t kUnits = (sizeof(T) - 256u * sizeof(uint2)) / 16u;  // 16-byte pieces
+  static constexpr std::uint32_t kPer = (kUnits + NT - 1u) / NT;
   uint4 v[kPer];
 };
-template <int FMT>
-__device__ __forceinline__ void iq_grid_issue(IqGridStage<FMT>& g, std::uint32_t tid, std::uint32_t nt) {
-  constexpr std::uint32_t U = IqGridStage<FMT>::kUnits;
-  const uint4* src = reinterpret_cast<const uint4*>(fmt_is_iq2s(FMT) ? static_cast<const void*>(&kIq2sImage)
-                                                                      : static_cast<const void*>(&kIq3sImage));
+template <class T, std::uint32_t NT>
+__device__ __forceinline__ void lds_grid_issue(LdsGridStage<T, NT>& g, const void* image, std::uint32_t tid,
+                                               std::uint32_t nt) {
+  constexpr std::uint32_t U = LdsGridStage<T, NT>::kUnits;
+  const uint4* src = static_cast<const uint4*>(image);
 #pragma unroll
-  for (std::uint32_t j = 0; j < IqGridStage<FMT>::kPer; ++j) {
+  for (std::uint32_t j = 0; j < LdsGridStage<T, NT>::kPer; ++j) {
     const std::uint32_t c = tid + j * nt;
     g.v[j] = src[c < U ? c : U - 1u];
   }
-  __builtin_amdgcn_sched_barrier(0);  // issued here, ahead of the later loads (not next to their writes)
+  __builtin_amdgcn_sched_barrier(0);  // issued here, ahead of the later loads
 }
 constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt left alone
-template <int FMT>
-__device__ __forceinline__ void iq_lds_commit(IqLds<FMT>& t, const IqGridStage<FMT>& g, std::uint32_t tid,
-                                              std::uint32_t nt) {
-  constexpr std::uint32_t U = IqGridStage<FMT>::kUnits;
+template <class T, std::uint32_t NT>
+__device__ __forceinline__ void lds_grid_commit(T& t, const LdsGridStage<T, NT>& g, const void* image,
+                                                std::uint32_t tid, std::uint32_t nt) {
+  constexpr std::uint32_t U = LdsGridStage<T, NT>::kUnits;
+  constexpr std::uint32_t P = LdsGridStage<T, NT>::kPer;
   uint4* dst = reinterpret_cast<uint4*>(&t);
 #pragma unroll
-  for (std::uint32_t j = 0; j < IqGridStage<FMT>::kPer; ++j) {
-    // no branch (the load would move into it): a re-read last piece is
-    // stored again, the same bytes to the same place
+  for (std::uint32_t j = 0; j < P; ++j) {
     const std::uint32_t c = tid + j * nt;
     dst[c < U ? c : U - 1u] = g.v[j];
   }
+  const uint4* src = static_cast<const uint4*>(image);
+  for (std::uint32_t c = tid + P * nt; c < U; c += nt) dst[c] = src[c];  // workgroups under NT threads
   for (std::uint32_t e = tid; e < 256u; e += nt) t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+template <int FMT>
+using IqGridStage = LdsGridStage<IqLds<FMT>, 128u>;
+template <int FMT>
+__device__ __forceinline__ const void* iq_image() {
+  return fmt_is_iq2s(FMT) ? static_cast<const void*>(&kIq2sImage) : static_cast<const void*>(&kIq3sImage);
 }
 
 // ---- per-format unit load + compute ------------------------------------------
@@ -780,7 +788,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   IqGridStage<FMT> grid_stage;
   if constexpr (fmt_is_iq(FMT)) {
     tables = &iq_lds<FMT>();
-    iq_grid_issue<FMT>(grid_stage, threadIdx.x, blockDim.x);
+    lds_grid_issue(grid_stage, iq_image<FMT>(), threadIdx.x, blockDim.x);
   }
   XG x0[UPL], x1[UPL];
 #pragma unroll
@@ -804,7 +812,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   // each row group keeps one tile of weights in flight.
   UnitRaw buf[2][TILE][UPL];
   load_tile(tile_of(0u), buf[0]);
-  if constexpr (fmt_is_iq(FMT)) iq_lds_commit<FMT>(*tables, grid_stage, threadIdx.x, blockDim.x);
+  if constexpr (fmt_is_iq(FMT)) lds_grid_commit(*tables, grid_stage, iq_image<FMT>(), threadIdx.x, blockDim.x);
   if constexpr (EpiHasReady<Epi>::value) epi.ready(lane);
   IqLaneScale ls[UPL];
   if constexpr (fmt_is_iq(FMT)) {
