@@ -77,6 +77,21 @@ def test_matvec_config_shapes(orc, fmt, shape):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", [F.IQ2S, F.IQ3S, F.IQ2S_UNITS, F.IQ3S_UNITS], ids=lambda f: F.NAMES[f])
+def test_matvec_iq_one_wave_workgroups(orc, fmt):
+    """2048 columns fit one wave per row (one column split), and past 16384 rows
+    the IQ matvecs run a persistent grid of one-row-group workgroups: one-wave
+    workgroups, whose codebook fill takes more pieces per thread than the
+    two-wave layout it is sized for."""
+    rows, cols = 32768, 2048
+    pack = packs.make_pack(fmt, rows, cols, seed=0x1A0E + fmt)
+    x = packs.normal_f32(0x1A0F + fmt, cols)
+    y = ops.matvec(ops.DevicePack(pack), ops.to_dev(x)).cpu().numpy()
+    of, pl, mt = oracle_args(pack)
+    ref = orc.matvec_f32(of, pl, mt, x, rows, cols, 8)
+    assert rel_err(y, ref) <= TOL
+
+
 def test_matvec_q4k_4096_config0(orc):
     rows = cols = 4096
     for fmt in (F.Q4K_SPLIT_NATIVE, F.Q4K_SPLIT_PREDECODED, F.Q4K_SPLIT_COMPACT, F.Q4K_SPLIT_HALF):
