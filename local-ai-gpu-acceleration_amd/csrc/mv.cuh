@@ -202,16 +202,14 @@ __device__ __forceinline__ IqLds<FMT>& iq_lds() {
 //  * lds_grid_commit, after the activation and first-tile loads are issued,
 //    writes the pieces to LDS (smaller workgroups add the rest piece by
 //    piece), computes the sign table (which keeps 2 KB per workgroup off the
-//    L2), waits for its LDS writes and meets the workgroup's other waves at the
-//    barrier.
+//    L2) and meets the workgroup's other waves at the barrier.
 // The compiler counts these plain loads exactly, so the writes wait for the
-// grid loads only: the activation and the first tile stay in flight through
-// the barrier, and the first round starts on the rows that have arrived. A
-// __syncthreads() (a workgroup fence) would wait for all of them, and so would
-// a read after a direct-to-LDS copy (the compiler waits for every outstanding
-// load there). The writes carry no branch (a load would move into it): a
-// re-read last piece is stored again, the same bytes to the same place. The
-// empty asm statements keep LDS accesses on their side of the bare s_barrier.
+// grid loads only, and the barrier for the LDS writes: the activation and the
+// first tile stay in flight through it, and the first round starts on the rows
+// that have arrived. After a direct-to-LDS copy the barrier would wait for
+// every outstanding load (the compiler cannot tell the copy's completion from
+// the later loads'). The writes carry no branch (a load would move into it): a
+// re-read last piece is stored again, the same bytes to the same place.
 template <class T, std::uint32_t NT>
 struct LdsGridStage {
   static constexpr std::uint32_t kUnits = (sizeof(T) - 256u * sizeof(uint2)) / 16u;  // 16-byte pieces
@@ -230,7 +228,6 @@ __device__ __forceinline__ void lds_grid_issue(LdsGridStage<T, NT>& g, const voi
   }
   __builtin_amdgcn_sched_barrier(0);  // issued here, ahead of the later loads
 }
-constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt left alone
 template <class T, std::uint32_t NT>
 __device__ __forceinline__ void lds_grid_commit(T& t, const LdsGridStage<T, NT>& g, const void* image,
                                                 std::uint32_t tid, std::uint32_t nt) {
@@ -245,10 +242,7 @@ __device__ __forceinline__ void lds_grid_commit(T& t, const LdsGridStage<T, NT>&
   const uint4* src = static_cast<const uint4*>(image);
   for (std::uint32_t c = tid + P * nt; c < U; c += nt) dst[c] = src[c];  // workgroups under NT threads
   for (std::uint32_t e = tid; e < 256u; e += nt) t.sign[e] = make_uint2(iq_sign_mask(e & 15u), iq_sign_mask(e >> 4));
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  __syncthreads();
 }
 template <int FMT>
 using IqGridStage = LdsGridStage<IqLds<FMT>, 128u>;
