@@ -158,6 +158,15 @@ struct EpiGateUp {
   }
 };
 
+// The same epilogue for hidden sizes of at most kShareXCols: workgroups of up
+// to 16 waves (one per CU at the 8B shapes) share one LDS copy of the staged
+// input and of the codebook, their row groups handing over column-split
+// partials pairwise.
+struct EpiGateUpWide : EpiGateUp {
+  static constexpr std::uint32_t kWaves = 16;
+  static constexpr bool kShareX = true;
+};
+
 // Logits and the greedy argmax: each row group keeps the best key of its tiles
 // in a register and stores it once, after its last tile, into its own slot;
 // the finalize kernel reduces the slots (no atomics, no per-tile reads).
@@ -745,6 +754,11 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
   const QTensor w{payload, meta, rows, cols};
   EpiGateUp e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.act = act;
+  if (cols <= kShareXCols) {
+    EpiGateUpWide ew{};
+    static_cast<EpiGateUp&>(ew) = e;
+    return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, ew, stream);
+  }
   return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, e, stream);
 }
 

@@ -687,6 +687,57 @@ struct EpiHasFinish<E, std::void_t<decltype(E::kFinish)>> {
   static constexpr bool value = E::kFinish;
 };
 
+// Plain epilogues that declare kWaves (> kMaxKs) run in workgroups of up to
+// kWaves waves whose row groups do not wait for each other: the column-split
+// waves of one row group hand over their partials through LDS counters
+// (pair_publish / pair_wait) instead of a workgroup barrier, so one workgroup
+// can hold many row groups without running them in lockstep.
+template <class E, class = void>
+struct EpiWaves {
+  static constexpr std::uint32_t value = kMaxKs;
+};
+template <class E>
+struct EpiWaves<E, std::void_t<decltype(E::kWaves)>> {
+  static constexpr std::uint32_t value = E::kWaves;
+};
+
+// Epilogues that declare kShareX read a staged x of at most kShareXCols
+// columns (the launcher's guarantee) from one LDS copy per workgroup, made in
+// the prologue, instead of every wave loading its own slice: the CU's load
+// path then carries the activation once per workgroup.
+constexpr std::uint32_t kShareXCols = 4096;
+template <class E, class = void>
+struct EpiShareX {
+  static constexpr bool value = false;
+};
+template <class E>
+struct EpiShareX<E, std::void_t<decltype(E::kShareX)>> {
+  static constexpr bool value = E::kShareX;
+};
+
+// A wave waits until the LDS counter reaches `target`, sleeping between reads.
+// The counters only grow and each is advanced by a wave of the same workgroup
+// that runs the same rounds, so the wait ends; the spin limit (~10^6 sleeps)
+// only bounds a wave's time if that ever failed. Counter updates go to LDS in
+// the wave's program order, after the data they announce (the empty asm
+// statements keep the compiler from moving LDS accesses across them).
+constexpr std::uint32_t kPairSpinLimit = 1u << 20;
+__device__ __forceinline__ void pair_wait(const std::uint32_t* counter, std::uint32_t target) {
+  asm volatile("" ::: "memory");
+  for (std::uint32_t i = 0; i < kPairSpinLimit; ++i) {
+    const std::uint32_t c = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (c >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void pair_publish(std::uint32_t* counter, std::uint32_t value) {
+  asm volatile("" ::: "memory");
+  __hip_atomic_store(counter, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  asm volatile("" ::: "memory");
+}
+
 // UPL units (32 columns each) per lane; a row's `cols / 32` units are split over
 // ks waves of one workgroup, which also holds nrg row groups (blockDim.x = 64 *
 // ks * nrg, ks * nrg <= 8). Each row group loads the next tile's rows before it
@@ -701,16 +752,26 @@ struct EpiHasFinish<E, std::void_t<decltype(E::kFinish)>> {
 //    hands all GR of them to epi.group(), inside the workgroup: no other
 //    workgroup's results are needed, so no device-wide synchronisation.
 template <int FMT, int UPL, int TILE, bool SELF, class Epi>
-__global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows, std::uint32_t ks,
-                                                  Epi epi_arg) {
+__global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows,
+                                                                      std::uint32_t ks, Epi epi_arg) {
   static_assert(Epi::kTile == TILE, "epilogue tile");
   constexpr std::uint32_t GR = EpiGroupRows<Epi>::value;
   static_assert(GR % TILE == 0u, "epilogue group of whole tiles");
   constexpr std::uint32_t TG = GR > 0u ? GR / TILE : 1u;  // tiles per group
+  constexpr std::uint32_t WMAX = EpiWaves<Epi>::value;
+  constexpr bool kPair = WMAX > static_cast<std::uint32_t>(kMaxKs);
+  static_assert(!kPair || GR == 0u, "pairwise hand-over for plain epilogues");
+  constexpr bool kShareX = EpiShareX<Epi>::value && !SELF;
   Epi epi = epi_arg;
   // Column-split partials, one slot per wave, double buffered by round parity
   // so a fast wave cannot overwrite a slot another wave still reads.
-  __shared__ float part[2][kMaxKs][TILE];
+  __shared__ float part[2][WMAX][TILE];
+  // Pairwise hand-over: ready[w] = rounds wave w has published, taken[w] =
+  // rounds the row group's epilogue wave w has consumed.
+  __shared__ std::uint32_t ready[kPair ? WMAX : 1u], taken[kPair ? WMAX : 1u];
+  // The workgroup's copy of the staged x (kShareX), in its global layout.
+  constexpr std::uint32_t kXPieces = kShareX ? static_cast<std::uint32_t>(xq_bytes(kShareXCols) / 16u) : 1u;
+  __shared__ uint4 xshare[kXPieces];
   // Grouped epilogues: a group's results, double buffered by group parity.
   __shared__ float gbuf[2][GR > 0u ? GR : 1u];
   const std::uint32_t lane = threadIdx.x & 63u;
@@ -779,10 +840,24 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   // loads only and leaves the activation and the weights in flight.
   epi.init(lane);
   IqLds<FMT>* tables = nullptr;
-  IqGridStage<FMT> grid_stage;
+  LdsGridStage<IqLds<FMT>, kPair ? 64u * WMAX : 128u> grid_stage;
   if constexpr (fmt_is_iq(FMT)) {
     tables = &iq_lds<FMT>();
     lds_grid_issue(grid_stage, iq_image<FMT>(), threadIdx.x, blockDim.x);
+  }
+  // shared x: 16-byte pieces of the staged buffer, loaded here, written to LDS
+  // with the codebook (a thread past the buffer re-reads its last piece)
+  constexpr std::uint32_t kXPer = (kXPieces + 64u * WMAX - 1u) / (64u * WMAX);
+  const std::uint32_t xpieces = kShareX ? static_cast<std::uint32_t>(xq_bytes(w.cols) / 16u) : 1u;
+  uint4 xreg[kXPer];
+  if constexpr (kShareX) {
+    const uint4* src = reinterpret_cast<const uint4*>(xs.xq.h);
+#pragma unroll
+    for (std::uint32_t j = 0; j < kXPer; ++j) {
+      const std::uint32_t c = threadIdx.x + j * blockDim.x;
+      xreg[j] = src[c < xpieces ? c : xpieces - 1u];
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
   XG x0[UPL], x1[UPL];
 #pragma unroll
@@ -797,7 +872,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
         xg_stage<false>(xs.x, nullptr, g0, x0[i]);
         xg_stage<false>(xs.x, nullptr, g1, x1[i]);
       }
-    } else {
+    } else if constexpr (!kShareX) {
       xg_load(xs.xq, g0, x0[i]);
       xg_load(xs.xq, g1, x1[i]);
     }
@@ -806,7 +881,36 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
   // each row group keeps one tile of weights in flight.
   UnitRaw buf[2][TILE][UPL];
   load_tile(tile_of(0u), buf[0]);
+  if constexpr (kPair) {
+    ready[wave] = 0u;
+    taken[wave] = 0u;
+  }
+  if constexpr (kShareX) {
+#pragma unroll
+    for (std::uint32_t j = 0; j < kXPer; ++j) {
+      const std::uint32_t c = threadIdx.x + j * blockDim.x;
+      xshare[c < xpieces ? c : xpieces - 1u] = xreg[j];  // no branch, as for the codebook
+    }
+    for (std::uint32_t c = threadIdx.x + kXPer * blockDim.x; c < xpieces; c += blockDim.x)
+      xshare[c] = reinterpret_cast<const uint4*>(xs.xq.h)[c];
+  }
   if constexpr (fmt_is_iq(FMT)) lds_grid_commit(*tables, grid_stage, iq_image<FMT>(), threadIdx.x, blockDim.x);
+  else if constexpr (kPair || kShareX) __syncthreads();
+  if constexpr (kShareX) {
+    // the staged layout (h, m, l: cols bytes each; s, sum: cols / 16 floats)
+    const std::uint8_t* xb = reinterpret_cast<const std::uint8_t*>(xshare);
+    const std::uint32_t c = w.cols;
+    const XQ xl{reinterpret_cast<const std::int8_t*>(xb), reinterpret_cast<const std::int8_t*>(xb + c),
+                reinterpret_cast<const std::int8_t*>(xb + 2u * c), reinterpret_cast<const float*>(xb + 3u * c),
+                reinterpret_cast<const float*>(xb + 3u * c) + c / kXGroup};
+#pragma unroll
+    for (int i = 0; i < UPL; ++i) {
+      std::uint32_t g0, g1;
+      unit_groups<FMT>(ub[i], uk[i], g0, g1);
+      xg_load(xl, g0, x0[i]);
+      xg_load(xl, g1, x1[i]);
+    }
+  }
   if constexpr (EpiHasReady<Epi>::value) epi.ready(lane);
   IqLaneScale ls[UPL];
   if constexpr (fmt_is_iq(FMT)) {
@@ -814,9 +918,11 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     for (int i = 0; i < UPL; ++i) ls[i] = iq_lane_scale<FMT>(uk[i], x0[i], x1[i]);
   }
 
-  auto finish_tile = [&](std::uint32_t t, std::uint32_t parity, std::uint32_t gpar, const UnitRaw (&raw)[TILE][UPL]) {
+  auto finish_tile = [&](std::uint32_t sj, std::uint32_t t, std::uint32_t parity, std::uint32_t gpar,
+                         const UnitRaw (&raw)[TILE][UPL]) {
     // Every wave of the workgroup runs the same rounds, so the barrier below is
-    // uniform; waves without a tile this round still take part in it.
+    // uniform; waves without a tile this round still take part in it (and in
+    // the pairwise hand-over: every round is published and consumed).
     const bool active = t < tiles;
     float acc[TILE];
 #pragma unroll
@@ -855,11 +961,28 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
     constexpr std::uint32_t spread = 64u / TILE;
     const std::uint32_t r = lane / spread;
     if (ks > 1u) {
-      if ((lane % spread) == 0u) part[parity][wave][r] = v;
-      __syncthreads();
-      if (kw != 0u) return;
-      v = part[parity][wave][r];
-      for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
+      if constexpr (kPair) {
+        // round sj: the non-epilogue waves write slot parity once the
+        // epilogue wave has consumed round sj - 2 (the slot's last use), then
+        // announce it; the epilogue wave adds the row group's slots in wave
+        // order once all are announced (the same sum as below)
+        const std::uint32_t w0 = wave - kw;
+        if (kw != 0u) {
+          if (sj >= 2u) pair_wait(&taken[w0], sj - 1u);
+          if ((lane % spread) == 0u) part[parity][wave][r] = v;
+          pair_publish(&ready[wave], sj + 1u);
+          return;
+        }
+        for (std::uint32_t k = 1; k < ks; ++k) pair_wait(&ready[wave + k], sj + 1u);
+        for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
+        pair_publish(&taken[wave], sj + 1u);
+      } else {
+        if ((lane % spread) == 0u) part[parity][wave][r] = v;
+        __syncthreads();
+        if (kw != 0u) return;
+        v = part[parity][wave][r];
+        for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
+      }
     }
     if constexpr (GR > 0u) {
       if (active && (lane % spread) == 0u) gbuf[gpar][(t % TG) * TILE + r] = v;
@@ -900,7 +1023,7 @@ __global__ __launch_bounds__(64 * kMaxKs) void mv_kernel(QTensor w, XSrc xs, std
         default: __builtin_amdgcn_s_setprio(0); break;
       }
     }
-    finish_tile(tile_of(sj), sj & 1u, (sj >> rshift) & 1u, raw);
+    finish_tile(sj, tile_of(sj), sj & 1u, (sj >> rshift) & 1u, raw);
     group_end(sj);
   };
   std::uint32_t s = 0;

@@ -29,6 +29,9 @@ inline int num_cus() {
 //    (the kernel's occupancy, queried once per instantiation and block size),
 //    nrg = 1 for the IQ formats; each row group double-buffers its tiles and
 //    the workgroup copies its codebook once;
+//  * epilogues with pairwise hand-over (max_waves > 8) on large matrices: as
+//    many row groups per workgroup as max_waves allows, one workgroup per
+//    resident slot;
 //  * grouped epilogues (group_rows > 0): a group's tiles over as many row
 //    groups as fit in 8 waves (nrg divides the group's tile count) and the rest
 //    over consecutive rounds; one group per workgroup, or several in turn when
@@ -41,7 +44,7 @@ struct MvGeom {
 // resident(block_threads) = workgroups of that size resident per CU (0: unknown).
 template <class Resident>
 inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, std::uint32_t group_rows,
-                    Resident resident, MvGeom& g) {
+                    std::uint32_t max_waves, Resident resident, MvGeom& g) {
   const std::uint32_t units = cols / 32u;
   g.upl = units > 512u ? 2 : 1;
   g.ks = (units + 64u * g.upl - 1u) / (64u * g.upl);
@@ -61,7 +64,15 @@ inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, s
   }
   const std::uint32_t per_cu = static_cast<std::uint32_t>(resident(64u * g.ks * g.nrg));
   if (per_cu > 0u && grid > per_cu * cus) {
-    if (group_rows == 0u && fmt_is_iq(fmt) && g.nrg > 1u) {
+    const std::uint32_t nrg_wide = max_waves / g.ks;
+    const std::uint32_t per_cu_wide =
+        max_waves > static_cast<std::uint32_t>(kMaxKs) && nrg_wide > g.nrg
+            ? static_cast<std::uint32_t>(resident(64u * g.ks * nrg_wide))
+            : 0u;
+    if (group_rows == 0u && per_cu_wide > 0u) {
+      g.nrg = nrg_wide;
+      grid = per_cu_wide * cus;
+    } else if (group_rows == 0u && fmt_is_iq(fmt) && g.nrg > 1u) {
       g.nrg = 1u;
       const std::uint32_t per_cu1 = static_cast<std::uint32_t>(resident(64u * g.ks));
       grid = (per_cu1 > 0u ? per_cu1 : 1u) * cus;
@@ -77,9 +88,10 @@ inline bool mv_geom(int fmt, std::uint32_t rows, std::uint32_t cols, int tile, s
 // (cached; 0 if the query fails).
 template <int FMT, int UPL, int TILE, bool SELF, class Epi>
 inline int mv_resident(std::uint32_t block_threads) {
-  static int cache[kMaxKs + 1] = {};
+  constexpr std::uint32_t kW = EpiWaves<Epi>::value;
+  static int cache[kW + 1] = {};
   const std::uint32_t w = block_threads / 64u;
-  if (w == 0u || w > static_cast<std::uint32_t>(kMaxKs)) return 0;
+  if (w == 0u || w > kW) return 0;
   if (cache[w] == 0) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -98,7 +110,7 @@ inline bool mv_geometry_fmt(std::uint32_t rows, std::uint32_t cols, MvGeom& g) {
   auto resident = [units](std::uint32_t threads) {
     return units > 512u ? mv_resident<FMT, 2, kT, SELF, Epi>(threads) : mv_resident<FMT, 1, kT, SELF, Epi>(threads);
   };
-  return mv_geom(FMT, rows, cols, kT, EpiGroupRows<Epi>::value, resident, g);
+  return mv_geom(FMT, rows, cols, kT, EpiGroupRows<Epi>::value, EpiWaves<Epi>::value, resident, g);
 }
 
 template <int FMT, bool SELF, class Epi>

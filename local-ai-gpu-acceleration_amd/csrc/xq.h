@@ -91,7 +91,7 @@ struct XQOut {
   float* sum;
 };
 
-__host__ __device__ inline std::size_t xq_bytes(std::uint32_t cols) {
+__host__ __device__ constexpr std::size_t xq_bytes(std::uint32_t cols) {
   return 3u * static_cast<std::size_t>(cols) + 8u * static_cast<std::size_t>(cols / kXGroup);
 }
 

@@ -71,9 +71,15 @@ def test_device_synth_matches_host_generator():
     m.close()
 
 
-@pytest.mark.parametrize("pos", [0, 37, 200])
-def test_decode_step_matches_oracle(orc, pos):
-    s = SMALL
+# hidden above 4096: gate_up's input is read per wave rather than from one shared
+# LDS copy per workgroup (kShareXCols), a different matvec instantiation
+HIDDEN_4608 = Shape(hidden=4608, n_heads=4, n_kv_heads=2, ffn=1024, vocab=1000, n_layers=1, max_ctx=256,
+                    page_size=16)
+
+
+@pytest.mark.parametrize("s,pos", [(SMALL, 0), (SMALL, 37), (SMALL, 200), (HIDDEN_4608, 37)],
+                         ids=["small-0", "small-37", "small-200", "hidden4608-37"])
+def test_decode_step_matches_oracle(orc, s, pos):
     m = build(s, pos)
     token = 123
     m.set_token_pos(token, pos)
