@@ -650,7 +650,7 @@ __device__ __forceinline__ float tile_reduce(float (&acc)[T], std::uint32_t lane
 
 // ---- the kernel -------------------------------------------------------------
 
-constexpr int kMaxKs = 8;  // waves per workgroup (and column-split partial slots)
+constexpr int kMaxKs = 8;  // waves per workgroup unless the epilogue declares kWaves
 
 // Rows per epilogue group: epilogues that declare kGroupRows (a multiple of
 // their tile) receive the results of kGroupRows consecutive rows at once.
@@ -740,8 +740,9 @@ __device__ __forceinline__ void pair_publish(std::uint32_t* counter, std::uint32
 
 // UPL units (32 columns each) per lane; a row's `cols / 32` units are split over
 // ks waves of one workgroup, which also holds nrg row groups (blockDim.x = 64 *
-// ks * nrg, ks * nrg <= 8). Each row group loads the next tile's rows before it
-// computes the current one. Tile schedule:
+// ks * nrg, ks * nrg <= 8, or <= kWaves for epilogues that declare it). Each
+// row group loads the next tile's rows before it computes the current one.
+// Tile schedule:
 //  * plain epilogues: row group rg of workgroup b handles tiles b + G * (rg +
 //    nrg * j), j = 0, 1, ... (G = gridDim.x), so tiles spread evenly over the
 //    CUs; the epilogue wave of the row group gets each tile's results;
