@@ -77,8 +77,15 @@ HIDDEN_4608 = Shape(hidden=4608, n_heads=4, n_kv_heads=2, ffn=1024, vocab=1000, 
                     page_size=16)
 
 
-@pytest.mark.parametrize("s,pos", [(SMALL, 0), (SMALL, 37), (SMALL, 200), (HIDDEN_4608, 37)],
-                         ids=["small-0", "small-37", "small-200", "hidden4608-37"])
+# gate_up of 65536 rows x 4096 columns: 8 rounds per row group in the 16-wave
+# workgroups, whose two column-split waves hand partials over through LDS
+# counters, reusing each double-buffered slot three times
+FFN_32768 = Shape(hidden=4096, n_heads=4, n_kv_heads=2, ffn=32768, vocab=1000, n_layers=1, max_ctx=256,
+                  page_size=16)
+
+
+@pytest.mark.parametrize("s,pos", [(SMALL, 0), (SMALL, 37), (SMALL, 200), (HIDDEN_4608, 37), (FFN_32768, 37)],
+                         ids=["small-0", "small-37", "small-200", "hidden4608-37", "ffn32768-37"])
 def test_decode_step_matches_oracle(orc, s, pos):
     m = build(s, pos)
     token = 123
