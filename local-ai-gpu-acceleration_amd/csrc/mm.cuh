@@ -323,12 +323,37 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t cols = w.cols, rows = w.rows, bpr = cols >> 8;
   const std::uint32_t q = lane >> 4, r16 = lane & 15u;
   const std::uint32_t tiles = (rows + 15u) >> 4;
+  const std::uint32_t nb = cols >> 8;  // 256-value blocks per row
+
+  // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
+  // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
+  // n = l % 16 = 2 s + hi/lo. blockDim.x being a multiple of 64, n and s are
+  // the same for all of a thread's elements; t_post is the sequence's RMSNorm
+  // scale (1 for a plainly staged input).
+  const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
+  const bool t_store = (t_n & 1u) == 0u && t_s < batch;
+  // Its inputs (eps and the sequence's per-block sums of squares from the
+  // staged tail) are read first and added once the weight loads are issued:
+  // a value used right away would make the wave wait for every load before
+  // it, here the B operands. Held as one vector value (no array the compiler
+  // could move to memory); inputs wider than 16 blocks add the rest later.
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  f32x16 t_ssv = {};
+  float t_eps = -1.0f;
+  if constexpr (!SELF) {
+    const X16Tail tail = x16_tail(x16, cols);
+    t_eps = *tail.eps;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const std::uint32_t bb = static_cast<std::uint32_t>(b) < nb ? static_cast<std::uint32_t>(b) : nb - 1u;
+      t_ssv[b] = tail.ss[t_s * nb + bb];
+    }
+  }
 
   // B operands of the panel: its blocks x 8 instructions, 1 KB of whole lanes each.
   // The lane's C column is n = lane % 16 = 2 s + hi/lo: its products of block
   // b of the panel carry that sequence's block exponent, 2^e[s][b].
   constexpr int PB = kPanelBlocks;
-  const std::uint32_t nb = cols >> 8;
   uint4 B[PB][8];
   float fb[PB];
   if constexpr (SELF) {
@@ -379,22 +404,6 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
     for (int b = 0; b < PB; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + PB * panel + b]);
   }
 
-  // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
-  // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
-  // n = l % 16 = 2 s + hi/lo. blockDim.x being a multiple of 64, n and s are
-  // the same for all of a thread's elements; t_post is the sequence's RMSNorm
-  // scale (1 for a plainly staged input).
-  const std::uint32_t t_n = (threadIdx.x >> 2) & 15u, t_s = t_n >> 1;
-  const bool t_store = (t_n & 1u) == 0u && t_s < batch;
-  float t_post = 1.0f;
-  if constexpr (!SELF) {
-    const X16Tail tail = x16_tail(x16, cols);
-    if (*tail.eps >= 0.0f) {
-      float ss = 0.0f;
-      for (std::uint32_t b = 0; b < nb; ++b) ss += tail.ss[t_s * nb + b];
-      t_post = 1.0f / sqrtf(ss / static_cast<float>(cols) + *tail.eps);
-    }
-  }
   epi.init(t_s);
 
   const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
@@ -432,6 +441,17 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   for (int j = 0; j < NB - 1; ++j) load_unit(static_cast<std::uint32_t>(j), ring[j]);
   if constexpr (fmt_is_iq(FMT))
     lds_grid_commit(mm_lds<FMT>(), grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
+  float t_post = 1.0f;
+  if constexpr (!SELF) {
+    if (t_eps >= 0.0f) {
+      float ss = 0.0f;  // in block order
+#pragma unroll
+      for (int b = 0; b < 16; ++b) ss += static_cast<std::uint32_t>(b) < nb ? t_ssv[b] : 0.0f;
+      const X16Tail tail = x16_tail(x16, cols);
+      for (std::uint32_t b = 16; b < nb; ++b) ss += tail.ss[t_s * nb + b];
+      t_post = 1.0f / sqrtf(ss / static_cast<float>(cols) + t_eps);
+    }
+  }
 
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto finish_unit = [&](std::uint32_t u, const MmRaw& raw) {
