@@ -860,18 +860,22 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  // Self-staging reads its fp32 groups here and converts them after the first
+  // tile's loads are issued: converting at once would make the first tile's
+  // request wait for these loads.
   XG x0[UPL], x1[UPL];
+  f32x16 xf0[UPL], xf1[UPL];
 #pragma unroll
   for (int i = 0; i < UPL; ++i) {
     std::uint32_t g0, g1;
     unit_groups<FMT>(ub[i], uk[i], g0, g1);
     if constexpr (SELF) {
       if (xs.x_aligned != 0u) {
-        xg_stage<true>(xs.x, nullptr, g0, x0[i]);
-        xg_stage<true>(xs.x, nullptr, g1, x1[i]);
+        xf0[i] = xg_read<true>(xs.x, g0);
+        xf1[i] = xg_read<true>(xs.x, g1);
       } else {
-        xg_stage<false>(xs.x, nullptr, g0, x0[i]);
-        xg_stage<false>(xs.x, nullptr, g1, x1[i]);
+        xf0[i] = xg_read<false>(xs.x, g0);
+        xf1[i] = xg_read<false>(xs.x, g1);
       }
     } else if constexpr (!kShareX) {
       xg_load(xs.xq, g0, x0[i]);
@@ -882,6 +886,14 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
   // each row group keeps one tile of weights in flight.
   UnitRaw buf[2][TILE][UPL];
   load_tile(tile_of(0u), buf[0]);
+  if constexpr (SELF) {
+    __builtin_amdgcn_sched_barrier(0);  // every load of the first tile issued before the conversion
+#pragma unroll
+    for (int i = 0; i < UPL; ++i) {
+      xg_quant(xf0[i], x0[i]);
+      xg_quant(xf1[i], x1[i]);
+    }
+  }
   if constexpr (kPair) {
     ready[wave] = 0u;
     taken[wave] = 0u;

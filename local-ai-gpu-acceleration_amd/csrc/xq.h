@@ -189,6 +189,33 @@ __device__ __forceinline__ void xg_stage(const float* __restrict__ x, const floa
   quant16(v, g);
 }
 
+// xg_stage without the multiplier, in two steps: the group's sixteen floats as
+// one vector value (xg_read), then the quant16 rule (xg_quant), so that a
+// caller can issue other loads between them. The same digits as xg_stage.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+template <bool ALIGNED = true>
+__device__ __forceinline__ f32x16 xg_read(const float* __restrict__ x, std::uint32_t group) {
+  f32x16 v;
+  if constexpr (ALIGNED) {
+    const float4* p = reinterpret_cast<const float4*>(x + kXGroup * group);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 t = p[i];
+      v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = x[kXGroup * group + i];
+  }
+  return v;
+}
+__device__ __forceinline__ void xg_quant(const f32x16& v, XG& g) {
+  float a[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) a[i] = v[i];
+  quant16(a, g);
+}
+
 __device__ __forceinline__ void xg_store(const XQOut& x, std::uint32_t group, const XG& g) {
   *reinterpret_cast<uint4*>(x.h + kXGroup * group) = make_uint4(g.h[0], g.h[1], g.h[2], g.h[3]);
   *reinterpret_cast<uint4*>(x.m + kXGroup * group) = make_uint4(g.m[0], g.m[1], g.m[2], g.m[3]);
