@@ -102,6 +102,7 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
     return;
   }
   float* const hs = a.h + static_cast<std::size_t>(s) * cols;
+  const float wmul = a.w != nullptr ? a.w[c] : 1.0f;  // read before the reductions' barriers
   float x;
   if (a.embed != nullptr) {
     const std::uint32_t tok = a.token[s] < a.vocab ? a.token[s] : a.vocab - 1u;
@@ -110,12 +111,24 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
   } else {
     x = hs[c];
   }
-  if (a.res != nullptr)
-    for (std::uint32_t g = 0; g < a.groups; ++g) x += a.res[(static_cast<std::size_t>(g) * a.batch + s) * cols + c];
+  if (a.res != nullptr) {
+    // the panel groups' partials, up to eight read at once (a runtime loop
+    // would wait for each before reading the next), added in group order
+    typedef float f32x8 __attribute__((ext_vector_type(8)));
+    f32x8 r;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const std::uint32_t gg = static_cast<std::uint32_t>(g) < a.groups ? static_cast<std::uint32_t>(g) : a.groups - 1u;
+      r[g] = a.res[(static_cast<std::size_t>(gg) * a.batch + s) * cols + c];
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) x = static_cast<std::uint32_t>(g) < a.groups ? x + r[g] : x;
+    for (std::uint32_t g = 8; g < a.groups; ++g) x += a.res[(static_cast<std::size_t>(g) * a.batch + s) * cols + c];
+  }
   if (a.embed != nullptr || a.res != nullptr) hs[c] = x;
   const float ss = block_reduce(x * x, part, false);
   if (threadIdx.x == 0u) x16_tail(a.x16, cols).ss[s * (cols / 256u) + b] = ss;
-  stage_block_value(a.w != nullptr ? x * a.w[c] : x, s, b, c, cols, a.x16, part);
+  stage_block_value(a.w != nullptr ? x * wmul : x, s, b, c, cols, a.x16, part);
 }
 
 // ---- batch epilogues --------------------------------------------------------
