@@ -611,6 +611,8 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
   token += blockIdx.x;
   if (pos != nullptr) pos += blockIdx.x;
   if (status != nullptr) status += blockIdx.x;
+  // the position, read before the reduction (only this kernel writes it, below)
+  const std::uint32_t p_now = (threadIdx.x == 0u && pos != nullptr) ? pos[0] : 0u;
   unsigned long long best = 0ull;
   for (std::uint32_t i0 = threadIdx.x; i0 < count; i0 += 256u * 8u) {
     unsigned long long k[8];
@@ -631,12 +633,12 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
   __syncthreads();
   if (threadIdx.x != 0u) return;
   for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
-  if (pos != nullptr && pos[0] >= capacity) {
+  if (pos != nullptr && p_now >= capacity) {
     if (status != nullptr) status[0] |= kStatusContextFull;
     return;
   }
   token[0] = best == 0ull ? 0u : 0xFFFFFFFFu - static_cast<std::uint32_t>(best & 0xFFFFFFFFull);
-  if (pos != nullptr) pos[0] += advance;
+  if (pos != nullptr) pos[0] = p_now + advance;
 }
 
 // ---- device-side synthetic packs ------------------------------------------------
