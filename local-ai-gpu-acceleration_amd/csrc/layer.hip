@@ -17,6 +17,7 @@
 #include "layer.h"
 #include "layer_common.cuh"
 #include "mv_launch.cuh"
+#include "mvq.cuh"
 #include "x16.h"
 
 namespace rtxllm {
@@ -766,6 +767,7 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
   const QTensor w{payload, meta, rows, cols};
   EpiGateUp e{};
   e.sumsq = in.sumsq, e.nslots = in.nslots, e.n = in.n, e.eps = in.eps, e.act = act;
+  if (mvq_fits(fmt, rows, cols)) return launch_mvq(fmt, w, xq_view(in.xq, cols), rows, e, stream);
   if (cols <= kShareXCols) {
     EpiGateUpWide ew{};
     static_cast<EpiGateUp&>(ew) = e;
