@@ -247,9 +247,18 @@ __global__ __launch_bounds__(64 * kMqMaxWaves) void mvq_kernel(QTensor w, XQ xq,
       const i32x4 c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i][1], w1, i32x4{0, 0, 0, 0}, 0, 0, 0);
       acc += mq_unit<FMT>(pair, i, mq_digits(c0), mq_digits(c1), ls[i]);
     }
+    // the row's sum over the four slices (lanes n, n + 16, n + 32, n + 48):
+    // with both operands v, a permlane swap leaves v and its partner 16 (32)
+    // lanes away in the two registers
     float v = acc * h2f(r.d);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    {
+      float a = v, b = v;
+      permlane16_swap(a, b);
+      v = a + b;
+      a = v, b = v;
+      permlane32_swap(a, b);
+      v = a + b;
+    }
     const std::uint32_t par = s & 1u;
     if (lane < kMqRows) part[par][wave][lane] = v;
     __syncthreads();
