@@ -32,8 +32,8 @@ def rel(a, b) -> float:
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-def build(shape: Shape, pos: int, seed: int = SEED, permute_pages: bool = True) -> Llama:
-    m = Llama(shape)
+def build(shape: Shape, pos: int, seed: int = SEED, permute_pages: bool = True, formats: dict | None = None) -> Llama:
+    m = Llama(shape, formats=formats)
     m.synth_weights(seed)
     torch.cuda.synchronize()
     H = shape.hidden
@@ -71,23 +71,30 @@ def test_device_synth_matches_host_generator():
     m.close()
 
 
-# hidden above 4096: gate_up's input is read per wave rather than from one shared
-# LDS copy per workgroup (kShareXCols), a different matvec instantiation
+# hidden above 4096: qkv / o read their input per wave rather than from one
+# shared LDS copy per workgroup (kShareXCols); gate_up runs on the matrix cores
+# with 9 panel waves per workgroup (8 at 4096, 1 at the small shape)
 HIDDEN_4608 = Shape(hidden=4608, n_heads=4, n_kv_heads=2, ffn=1024, vocab=1000, n_layers=1, max_ctx=256,
                     page_size=16)
 
 
-# gate_up of 65536 rows x 4096 columns: 8 rounds per row group in the 16-wave
-# workgroups, whose two column-split waves hand partials over through LDS
-# counters, reusing each double-buffered slot three times
+# gate_up of 65536 rows x 4096 columns: 8 rounds per workgroup of the
+# matrix-core matvec, reusing each double-buffered partials slot three times
 FFN_32768 = Shape(hidden=4096, n_heads=4, n_kv_heads=2, ffn=32768, vocab=1000, n_layers=1, max_ctx=256,
                   page_size=16)
 
 
-@pytest.mark.parametrize("s,pos", [(SMALL, 0), (SMALL, 37), (SMALL, 200), (HIDDEN_4608, 37), (FFN_32768, 37)],
-                         ids=["small-0", "small-37", "small-200", "hidden4608-37", "ffn32768-37"])
-def test_decode_step_matches_oracle(orc, s, pos):
-    m = build(s, pos)
+# gate_up in IQ3_S: the runner's IQ3S_UNITS copy on the matrix cores
+IQ3S_GATE_UP = dict(fmt_gate_up=F.IQ3S)
+
+
+@pytest.mark.parametrize("s,pos,formats", [(SMALL, 0, None), (SMALL, 37, None), (SMALL, 200, None),
+                                           (HIDDEN_4608, 37, None), (FFN_32768, 37, None), (SMALL, 37, IQ3S_GATE_UP),
+                                           (HIDDEN_4608, 37, IQ3S_GATE_UP)],
+                         ids=["small-0", "small-37", "small-200", "hidden4608-37", "ffn32768-37", "small-37-iq3s-ffn",
+                              "hidden4608-37-iq3s-ffn"])
+def test_decode_step_matches_oracle(orc, s, pos, formats):
+    m = build(s, pos, formats=formats)
     token = 123
     m.set_token_pos(token, pos)
     ref = HostModel(m, range(s.n_layers))
