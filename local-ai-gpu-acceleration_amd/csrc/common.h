@@ -29,6 +29,45 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v_permlane32_swap / v_permlane16_swap (gfx950): exchange a's upper 32 (odd
+// 16-lane rows') lanes with b's lower 32 (even rows') lanes. Issued as inline
+// asm: this compiler's __builtin_amdgcn_permlane{16,32}_swap treats the two
+// results as one value (it emitted a + a for the sum of both), so the builtin
+// is not usable. The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// Wave64 all-reduce of an exact, order-free operation on 32-bit patterns
+// (max, integer sum, or): DPP quad xor 1 and xor 2, row half mirror (lane
+// i <-> 7 - i), row mirror (i <-> 15 - i), then the 16- and 32-lane permlane
+// swaps; every lane receives the result, and no step goes through LDS. G = 8
+// stops after the half mirror: the result of each aligned group of 8 lanes.
+template <int CTRL>
+__device__ __forceinline__ std::uint32_t dpp_bits(std::uint32_t v) {
+  return static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int G = 64, class Op>
+__device__ __forceinline__ std::uint32_t lanes_reduce_exact(std::uint32_t v, Op op) {
+  static_assert(G == 8 || G == 64, "groups of 8 lanes or the wave");
+  v = op(v, dpp_bits<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_bits<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_bits<0x141>(v));  // row_half_mirror
+  if constexpr (G == 64) {
+    v = op(v, dpp_bits<0x140>(v));  // row_mirror
+    float a = __uint_as_float(v), b = a;
+    permlane16_swap(a, b);
+    v = op(__float_as_uint(a), __float_as_uint(b));
+    a = __uint_as_float(v), b = a;
+    permlane32_swap(a, b);
+    v = op(__float_as_uint(a), __float_as_uint(b));
+  }
+  return v;
+}
+
 // 6-bit scale / min of sub-block j of a K-quant block from its 12 packed scale
 // bytes held as three little-endian words (ggml get_scale_min_k4).
 __device__ __forceinline__ void scale_min_k4(int j, std::uint32_t s0, std::uint32_t s1, std::uint32_t s2,

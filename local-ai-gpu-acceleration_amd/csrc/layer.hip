@@ -24,9 +24,9 @@ namespace rtxllm {
 namespace {
 
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return static_cast<int>(lanes_reduce_exact(static_cast<std::uint32_t>(v), [](std::uint32_t a, std::uint32_t b) {
+    return a + b;  // two's complement: the same bits as the int sum
+  }));
 }
 
 // 1 / sqrt(sum / n + eps) from the producer's partial sums of squares, in two
@@ -520,23 +520,20 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   // Stage att for the o projection: the 16-value group of dims [16 k, 16 k + 16)
   // is held by lanes [8 k, 8 k + 8), two values each (the quant16 rule; max and
   // integer sum are order independent, so the digits equal quant16's).
-  float m = fmaxf(fabsf(a0), fabsf(a1));
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
-  m = fmaxf(m, __shfl_xor(m, 4, 64));
-  int nan = __builtin_isunordered(a0, a1) ? 1 : 0;
-  nan |= __shfl_xor(nan, 1, 64);
-  nan |= __shfl_xor(nan, 2, 64);
-  nan |= __shfl_xor(nan, 4, 64);
+  // the group's max |att|, NaN flag and integer sum over its 8 lanes (DPP, no LDS)
+  const float m = __uint_as_float(lanes_reduce_exact<8>(__float_as_uint(fmaxf(fabsf(a0), fabsf(a1))),
+                                                        [](std::uint32_t a, std::uint32_t b) {
+                                                          return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+                                                        }));
+  const std::uint32_t nan = lanes_reduce_exact<8>(__builtin_isunordered(a0, a1) ? 1u : 0u,
+                                                  [](std::uint32_t a, std::uint32_t b) { return a | b; });
   const XScale sc = xq_scale(m, nan != 0);
   const int X0 = xq_fixed(a0, sc), X1 = xq_fixed(a1, sc);
   int H0, M0, L0, H1, M1, L1;
   xq_digits(X0, H0, M0, L0);
   xq_digits(X1, H1, M1, L1);
-  int total = X0 + X1;
-  total += __shfl_xor(total, 1, 64);
-  total += __shfl_xor(total, 2, 64);
-  total += __shfl_xor(total, 4, 64);
+  const int total = static_cast<int>(lanes_reduce_exact<8>(static_cast<std::uint32_t>(X0 + X1),
+                                                           [](std::uint32_t a, std::uint32_t b) { return a + b; }));
   auto pair = [](int lo, int hi) {
     return static_cast<std::uint16_t>((static_cast<std::uint32_t>(lo) & 0xFFu) |
                                       ((static_cast<std::uint32_t>(hi) & 0xFFu) << 8));

@@ -9,9 +9,9 @@
 namespace rtxllm {
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return __uint_as_float(lanes_reduce_exact(__float_as_uint(v), [](std::uint32_t a, std::uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
 }
 
 // SiLU v / (1 + exp(-v)) (main.cpp:1435-1503), as v * sigmoid(v).

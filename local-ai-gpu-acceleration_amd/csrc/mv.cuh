@@ -585,18 +585,6 @@ constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor2 = 0x122;
 constexpr int kDppRowRor1 = 0x121;
 
-// v_permlane32_swap / v_permlane16_swap (gfx950): exchange a's upper 32 (odd
-// 16-lane rows') lanes with b's lower 32 (even rows') lanes. Issued as inline
-// asm: this compiler's __builtin_amdgcn_permlane{16,32}_swap treats the two
-// results as one value (it emitted a + a for the sum of both), so the builtin
-// is not usable. The s_nop covers the VALU-write -> permlane-read hazard.
-__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
 // acc[j] holds lane partials of row j (T in {4, 8, 16}); afterwards every lane
 // of [r * 64/T, (r+1) * 64/T) holds the full sum of row r. Each halving step
 // keeps one half of the live rows per lane group and adds the partner's
