@@ -22,12 +22,6 @@ __device__ __forceinline__ float f16_bits_to_f32(std::uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits)));
 }
 
-// Wave64 sum; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
 
 // v_permlane32_swap / v_permlane16_swap (gfx950): exchange a's upper 32 (odd
 // 16-lane rows') lanes with b's lower 32 (even rows') lanes. Issued as inline
@@ -41,8 +35,8 @@ __device__ __forceinline__ void permlane16_swap(float& a, float& b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
-// Wave64 all-reduce of an exact, order-free operation on 32-bit patterns
-// (max, integer sum, or): DPP quad xor 1 and xor 2, row half mirror (lane
+// Wave64 all-reduce of an operation on 32-bit patterns (exact and order-free
+// for max, integer sum, or; the fp32 sum below fixes this order): DPP quad xor 1 and xor 2, row half mirror (lane
 // i <-> 7 - i), row mirror (i <-> 15 - i), then the 16- and 32-lane permlane
 // swaps; every lane receives the result, and no step goes through LDS. G = 8
 // stops after the half mirror: the result of each aligned group of 8 lanes.
@@ -66,6 +60,15 @@ __device__ __forceinline__ std::uint32_t lanes_reduce_exact(std::uint32_t v, Op 
     v = op(__float_as_uint(a), __float_as_uint(b));
   }
   return v;
+}
+
+// Wave64 sum in the order of lanes_reduce_exact (DPP and permlane steps, no
+// LDS); every lane receives the same total (each step adds a + b in both
+// partners, and fp32 addition commutes).
+__device__ __forceinline__ float wave_sum(float v) {
+  return __uint_as_float(lanes_reduce_exact(__float_as_uint(v), [](std::uint32_t a, std::uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
 }
 
 // 6-bit scale / min of sub-block j of a K-quant block from its 12 packed scale
