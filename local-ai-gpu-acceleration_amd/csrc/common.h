@@ -62,6 +62,31 @@ __device__ __forceinline__ std::uint32_t lanes_reduce_exact(std::uint32_t v, Op 
   return v;
 }
 
+// The value of lane ^ M (the pairing of __shfl_xor with mask M, so sums and
+// maxima keep their bits) by DPP or a permlane swap instead of an LDS shuffle.
+// M = 4 takes lane - 4 or lane + 4 within the 16-lane row; every lane of the
+// wave must be active.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "a single-bit lane mask");
+  const std::uint32_t u = __float_as_uint(v);
+  if constexpr (M == 1) {
+    return __uint_as_float(dpp_bits<0xB1>(u));  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __uint_as_float(dpp_bits<0x4E>(u));  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const std::uint32_t down = dpp_bits<0x114>(u), up = dpp_bits<0x104>(u);  // row_shr:4, row_shl:4
+    return __uint_as_float((threadIdx.x & 4u) ? down : up);
+  } else if constexpr (M == 8) {
+    return __uint_as_float(dpp_bits<0x128>(u));  // row_ror:8
+  } else {
+    float a = v, b = v;
+    if constexpr (M == 16) permlane16_swap(a, b);  // a: rows 0, 0, 2, 2; b: rows 1, 1, 3, 3
+    else permlane32_swap(a, b);                     // a: lanes 0-31 twice; b: lanes 32-63 twice
+    return (threadIdx.x & static_cast<std::uint32_t>(M)) ? a : b;
+  }
+}
+
 // Wave64 sum in the order of lanes_reduce_exact (DPP and permlane steps, no
 // LDS); every lane receives the same total (each step adds a + b in both
 // partners, and fp32 addition commutes).

@@ -393,21 +393,21 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float t = sc[i] + __shfl_xor(sc[i], 1, 64);
+    const float t = sc[i] + lane_xor<1>(sc[i]);
     const bool valid = wp0 + 4u * qq + static_cast<std::uint32_t>(i) <= pos;
     s4[i] = valid ? t : -INFINITY;
     m = fmaxf(m, s4[i]);
   }
-  m = fmaxf(m, __shfl_xor(m, 16, 64));
-  m = fmaxf(m, __shfl_xor(m, 32, 64));  // head max over the wave's positions (-inf: none)
+  m = fmaxf(m, lane_xor<16>(m));
+  m = fmaxf(m, lane_xor<32>(m));  // head max over the wave's positions (-inf: none)
   float l = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     p4[i] = s4[i] == -INFINITY ? 0.0f : expf(s4[i] - m);
     l += p4[i];
   }
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l += lane_xor<16>(l);
+  l += lane_xor<32>(l);
   float o0[GROUP], o1[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
