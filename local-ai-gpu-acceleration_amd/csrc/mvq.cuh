@@ -5,8 +5,9 @@
 // of the staged activation in 24 v_dot4 per 32-value unit, about a third of
 // its VALU work. Here one v_mfma_i32_16x16x64_i8 does them for 16 rows at once:
 //  * B operand (weights): lane l = row l & 15 of a 16-row tile and slice
-//    q = l >> 4; the lane decodes 16 values of its row (half a unit) into the
-//    four words unit_lookup produces, exactly as mv_kernel does;
+//    q = l >> 4; per instruction the lane supplies 16 values of its row (half
+//    a unit) as four signed int8 words, decoded as mv_kernel's unit_lookup
+//    decodes them;
 //  * A operand (activation): A row m = 4 s + d carries digit d (H, M, L) of the
 //    16-value group that slice s of the B lanes holds, in slice s only, and
 //    zeros elsewhere (A rows 4 s + 3 are all zero);
@@ -35,7 +36,7 @@ namespace rtxllm {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr std::uint32_t kMqRows = 16;    // rows per tile
-constexpr std::uint32_t kMqUnits = 4;    // consecutive units per lane and tile (the scale loads assume 4)
+constexpr std::uint32_t kMqUnits = 4;    // consecutive units per lane and tile (the group-scale reads assume 4)
 constexpr std::uint32_t kMqPanel = 4u * kMqUnits * 32u;  // columns per wave
 constexpr std::uint32_t kMqMaxWaves = 16;
 
