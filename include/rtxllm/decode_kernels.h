@@ -239,6 +239,31 @@ hipError_t rtxllm_stage_activation(const float* x, const float* weight, uint32_t
 /* y[rows] = W x_hat for a staged x (the layer pipeline's matvec). */
 hipError_t rtxllm_matvec_xq(int format, const uint8_t* payload, const uint8_t* meta, const void* xq, float* y,
                             uint32_t rows, uint32_t cols, hipStream_t stream);
+/* The same on the int8 matrix cores (v_mfma_i32_16x16x64_i8 over 16-row
+ * tiles, one wave per 512-column panel), the kernel of the decode runner's
+ * batch-1 gate/up: IQ unit layouts only (formats 9, 10), rows % 16 == 0,
+ * cols % 512 == 0, cols <= 8192. Each 16-value group's integer dot is the
+ * exact one rtxllm_matvec_xq forms; the scaled group results are added in
+ * another order, so y agrees with rtxllm_matvec_xq to fp32 rounding, not bit
+ * for bit. */
+hipError_t rtxllm_matvec_xq_mfma(int format, const uint8_t* payload, const void* xq, float* y, uint32_t rows,
+                                 uint32_t cols, hipStream_t stream);
+
+/* The decode runner's fused gate/up stage. W [rows][cols] holds the gate and
+ * up rows interleaved (row 2i = gate_i, row 2i + 1 = up_i); with (g, u) =
+ * W x_hat for the staged xq and the RMSNorm scale s = 1 / sqrt(sum(sumsq[0 ..
+ * nslots)) / cols + eps) from the producer's partial sums of squares,
+ * act[i] = silu(s g_i) (s u_i), silu(v) = v / (1 + exp(-v)) (main.cpp:
+ * 1435-1503 for silu). Kernels: the matrix cores for the IQ unit layouts at
+ * rtxllm_matvec_xq_mfma's shapes; otherwise the dot-product matvec, for cols
+ * <= 4096 in one 16-wave workgroup per CU whose column-split waves hand their
+ * partials over through bounded LDS waits. A wait that ran out ORs
+ * RTXLLM_STATUS_WAIT_TIMEOUT into *status (status may be null) and act is
+ * then not valid. rows % 4 == 0. */
+#define RTXLLM_STATUS_WAIT_TIMEOUT 2u
+hipError_t rtxllm_gate_up_silu(int format, const uint8_t* payload, const uint8_t* meta, const void* xq,
+                               const float* sumsq, uint32_t nslots, float eps, float* act, uint32_t rows,
+                               uint32_t cols, uint32_t* status, hipStream_t stream);
 
 /* Batched matvec on the matrix cores: y[s][rows] = W x_s for s < batch <= 8
  * (the batch-8 decode variant). Formats: 0 Q4_K raw, 4 Q4_K split-native,

@@ -177,11 +177,15 @@ uint32_t rtxllm_llama_launches_per_step(const rtxllm_llama* m);
  * RTXLLM_LLAMA_STATUS_CONTEXT_FULL: a step ran while the sequence's position
  * was max_ctx (its KV cache full): that step had no slot for its token, so it
  * left the sequence's token and position as they were (the sequence halts at
- * max_ctx instead of decoding past the context end). The bit stays set until
- * cleared. rtxllm_llama_status copies the batch's words to host memory and
- * waits for the stream; rtxllm_llama_clear_status zeroes them (both
- * synchronous, not capture-safe). */
-enum { RTXLLM_LLAMA_STATUS_CONTEXT_FULL = 1 };
+ * max_ctx instead of decoding past the context end).
+ * RTXLLM_LLAMA_STATUS_WAIT_TIMEOUT (word 0): a bounded in-kernel wait of the
+ * batch-1 gate/up matvec ran out (its column-split waves hand partials over
+ * through LDS counters when a K-quant gate/up has hidden <= 4096), so that
+ * step's results are not valid. The bits stay set until cleared.
+ * rtxllm_llama_status copies the batch's words to host memory and waits for
+ * the stream; rtxllm_llama_clear_status zeroes them (both synchronous, not
+ * capture-safe). */
+enum { RTXLLM_LLAMA_STATUS_CONTEXT_FULL = 1, RTXLLM_LLAMA_STATUS_WAIT_TIMEOUT = 2 };
 hipError_t rtxllm_llama_status(rtxllm_llama* m, uint32_t* status, hipStream_t stream);
 hipError_t rtxllm_llama_clear_status(rtxllm_llama* m, hipStream_t stream);
 

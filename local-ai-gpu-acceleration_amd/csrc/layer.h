@@ -83,9 +83,16 @@ hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint
                            void* xq_next, float* sumsq_next, hipStream_t stream);
 
 // Rows interleaved gate / up (row 2i = gate_i, row 2i + 1 = up_i), x =
-// rmsnorm(h): act[i] = silu(gate_i) * up_i.
+// rmsnorm(h): act[i] = silu(gate_i) * up_i. Kernel: the int8 matrix cores for
+// the IQ unit layouts on whole 16-row tiles and 512-column panels; else the
+// dot-product matvec, for cols <= 4096 in one 16-wave workgroup per CU whose
+// column-split waves hand partials over through bounded LDS waits: a wait that
+// ran out ORs kStatusWaitTimeout into *status (status may be null).
+// wait_limit / wait_bias: reads per wait and a bias on its target (production:
+// kPairSpinLimit and 0; a test forces the timeout with a bias no wave reaches).
 hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                          std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream);
+                          std::uint32_t cols, const NormIn& in, float* act, std::uint32_t* status,
+                          hipStream_t stream, std::uint32_t wait_limit = 1u << 20, std::uint32_t wait_bias = 0u);
 
 // logits = W rmsnorm(h), and per row group of the launch the best argmax key
 // (ordered(logit) << 32 | ~row: greedy argmax, lowest index on ties, NaN never
@@ -97,6 +104,7 @@ hipError_t launch_logits(int fmt, const std::uint8_t* payload, const std::uint8_
                          std::uint32_t key_capacity, std::uint32_t* key_count, hipStream_t stream);
 
 // Status bit of a sequence whose step ran at a position >= the KV capacity.
+// (Bit 2, kStatusWaitTimeout of mv.cuh: a bounded in-kernel wait ran out.)
 constexpr std::uint32_t kStatusContextFull = 1u;
 
 // token[0] = argmax over keys[0, count) (0 if every logit was NaN); *pos +=

@@ -162,10 +162,12 @@ struct EpiGateUp {
 // The same epilogue for hidden sizes of at most kShareXCols: workgroups of up
 // to 16 waves (one per CU at the 8B shapes) share one LDS copy of the staged
 // input and of the codebook, their row groups handing over column-split
-// partials pairwise.
+// partials pairwise (a hand-over wait that runs out sets kStatusWaitTimeout in
+// *wait.status).
 struct EpiGateUpWide : EpiGateUp {
   static constexpr std::uint32_t kWaves = 16;
   static constexpr bool kShareX = true;
+  PairWait wait;
 };
 
 // Logits and the greedy argmax: each row group keeps the best key of its tiles
@@ -759,7 +761,8 @@ hipError_t launch_residual(int fmt, const std::uint8_t* payload, const std::uint
 }
 
 hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8_t* meta, std::uint32_t rows,
-                          std::uint32_t cols, const NormIn& in, float* act, hipStream_t stream) {
+                          std::uint32_t cols, const NormIn& in, float* act, std::uint32_t* status,
+                          hipStream_t stream, std::uint32_t wait_limit, std::uint32_t wait_bias) {
   if ((rows % 4u) != 0u || in.nslots == 0u) return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   EpiGateUp e{};
@@ -768,6 +771,7 @@ hipError_t launch_gate_up(int fmt, const std::uint8_t* payload, const std::uint8
   if (cols <= kShareXCols) {
     EpiGateUpWide ew{};
     static_cast<EpiGateUp&>(ew) = e;
+    ew.wait.status = status, ew.wait.limit = wait_limit, ew.wait.bias = wait_bias;
     return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, ew, stream);
   }
   return launch_mv<false>(fmt, w, staged_src(xq_view(in.xq, cols)), rows, e, stream);

@@ -1,9 +1,16 @@
 // Batch-1 matvec and dequant entry points (C-ABI) for the GGUF resident packs.
 #include "rtxllm/decode_kernels.h"
 
+#include "rtxllm/testing.h"
+
 #include "internal.h"
 #include "dequant.cuh"
+#include "layer.h"
 #include "mv_launch.cuh"
+#include "mvq.cuh"
+
+static_assert(rtxllm::kPairSpinLimit == (1u << 20), "launch_gate_up's default wait limit");
+static_assert(rtxllm::kStatusWaitTimeout == RTXLLM_STATUS_WAIT_TIMEOUT, "status bit of the C-ABI");
 
 namespace rtxllm {
 namespace {
@@ -187,6 +194,47 @@ extern "C" hipError_t rtxllm_matvec_xq(int format, const std::uint8_t* payload, 
     return hipErrorInvalidValue;
   const QTensor w{payload, meta, rows, cols};
   return launch_mv<false>(format, w, staged_src(xq_view(xq, cols)), rows, EpiStore<kTile>{y}, stream);
+}
+
+extern "C" hipError_t rtxllm_matvec_xq_mfma(int format, const std::uint8_t* payload, const void* xq, float* y,
+                                            std::uint32_t rows, std::uint32_t cols, hipStream_t stream) {
+  if (!mvq_fits(format, rows, cols) || payload == nullptr || xq == nullptr || y == nullptr ||
+      !pointers_ok(format, payload, nullptr, xq, true))
+    return hipErrorInvalidValue;
+  const QTensor w{payload, nullptr, rows, cols};
+  return launch_mvq(format, w, xq_view(xq, cols), rows, EpiStore<kTile>{y}, stream);
+}
+
+namespace {
+hipError_t gate_up_call(int format, const std::uint8_t* payload, const std::uint8_t* meta, const void* xq,
+                        const float* sumsq, std::uint32_t nslots, float eps, float* act, std::uint32_t rows,
+                        std::uint32_t cols, std::uint32_t* status, hipStream_t stream, std::uint32_t wait_limit,
+                        std::uint32_t wait_bias) {
+  if (!shape_ok(rows, cols) || (rows % 4u) != 0u || payload == nullptr || xq == nullptr || sumsq == nullptr ||
+      nslots == 0u || act == nullptr || (needs_meta(format) && meta == nullptr) ||
+      !pointers_ok(format, payload, meta, xq, true) || wait_limit == 0u)
+    return hipErrorInvalidValue;
+  const NormIn in{xq, sumsq, nslots, cols, eps};
+  return launch_gate_up(format, payload, meta, rows, cols, in, act, status, stream, wait_limit, wait_bias);
+}
+}  // namespace
+
+extern "C" hipError_t rtxllm_gate_up_silu(int format, const std::uint8_t* payload, const std::uint8_t* meta,
+                                          const void* xq, const float* sumsq, std::uint32_t nslots, float eps,
+                                          float* act, std::uint32_t rows, std::uint32_t cols, std::uint32_t* status,
+                                          hipStream_t stream) {
+  return gate_up_call(format, payload, meta, xq, sumsq, nslots, eps, act, rows, cols, status, stream,
+                      kPairSpinLimit, 0u);
+}
+
+extern "C" hipError_t rtxllm_test_gate_up_silu_waits(int format, const std::uint8_t* payload,
+                                                     const std::uint8_t* meta, const void* xq, const float* sumsq,
+                                                     std::uint32_t nslots, float eps, float* act, std::uint32_t rows,
+                                                     std::uint32_t cols, std::uint32_t* status,
+                                                     std::uint32_t wait_limit, std::uint32_t wait_bias,
+                                                     hipStream_t stream) {
+  return gate_up_call(format, payload, meta, xq, sumsq, nslots, eps, act, rows, cols, status, stream, wait_limit,
+                      wait_bias);
 }
 
 // ---- reference-named matvec launchers --------------------------------------

@@ -28,6 +28,9 @@
 #include "synth.h"
 #include "xq.h"
 
+static_assert(RTXLLM_LLAMA_STATUS_CONTEXT_FULL == rtxllm::kStatusContextFull, "status bits of the C-ABI");
+static_assert(RTXLLM_LLAMA_STATUS_WAIT_TIMEOUT == RTXLLM_STATUS_WAIT_TIMEOUT, "status bits of the C-ABI");
+
 struct rtxllm_llama {
   rtxllm_llama_config cfg{};
   rtxllm::VramSuperallocator arena;
@@ -800,7 +803,8 @@ hipError_t launch_stage(rtxllm_llama* m, std::uint32_t l, int stage, bool embed,
     case kGateUp: {
       int f = 0;
       const TensorRef t = tensor_for(m, "gate_up", l, c.fmt_gate_up, f);
-      return rtxllm::launch_gate_up(f, t.payload, t.meta, 2u * c.ffn, c.hidden, in, region<float>(m, "act"), stream);
+      return rtxllm::launch_gate_up(f, t.payload, t.meta, 2u * c.ffn, c.hidden, in, region<float>(m, "act"),
+                                    region<std::uint32_t>(m, "status"), stream);
     }
     case kDown: {
       int f = 0;

@@ -703,23 +703,47 @@ struct EpiShareX<E, std::void_t<decltype(E::kShareX)>> {
   static constexpr bool value = E::kShareX;
 };
 
-// A wave waits until the LDS counter reaches `target`, sleeping between reads.
-// The counters only grow and each is advanced by a wave of the same workgroup
-// that runs the same rounds, so the wait ends; the spin limit (~10^6 sleeps)
-// only bounds a wave's time if that ever failed. Counter updates go to LDS in
-// the wave's program order, after the data they announce (the empty asm
-// statements keep the compiler from moving LDS accesses across them).
+// A wave waits until the LDS counter reaches `target`, sleeping between reads,
+// for at most `limit` reads, and returns whether the counter got there. The
+// counters only grow and each is advanced by a wave of the same workgroup that
+// runs the same rounds, so the wait ends; the limit (kPairSpinLimit, ~10^6
+// sleeps) only bounds a wave's time if that ever failed, and the kernel then
+// reports it (PairWait::status) instead of passing a stale partial on
+// silently. Counter updates go to LDS in the wave's program order, after the
+// data they announce (the empty asm statements keep the compiler from moving
+// LDS accesses across them).
 constexpr std::uint32_t kPairSpinLimit = 1u << 20;
-__device__ __forceinline__ void pair_wait(const std::uint32_t* counter, std::uint32_t target) {
+__device__ __forceinline__ bool pair_wait(const std::uint32_t* counter, std::uint32_t target, std::uint32_t limit) {
   asm volatile("" ::: "memory");
-  for (std::uint32_t i = 0; i < kPairSpinLimit; ++i) {
+  bool reached = false;
+  for (std::uint32_t i = 0; i < limit; ++i) {
     const std::uint32_t c = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (c >= target) break;
+    if (c >= target) {
+      reached = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   asm volatile("" ::: "memory");
+  return reached;
 }
+
+// Status bit set when a bounded wait of a kernel ran out: that launch's
+// results are not valid.
+constexpr std::uint32_t kStatusWaitTimeout = 2u;
+
+// What an epilogue with the pairwise hand-over (kWaves) carries as `wait`:
+// the status word that gets kStatusWaitTimeout if any wave's wait ran out
+// (null: not reported), the wait limit (kPairSpinLimit) and a bias added to
+// every wait target (0; a host-side test sets it to make every wait run out
+// after `limit` reads, so that the report can be checked while each wave
+// still finishes its rounds).
+struct PairWait {
+  std::uint32_t* status = nullptr;
+  std::uint32_t limit = kPairSpinLimit;
+  std::uint32_t bias = 0u;
+};
 __device__ __forceinline__ void pair_publish(std::uint32_t* counter, std::uint32_t value) {
   asm volatile("" ::: "memory");
   __hip_atomic_store(counter, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -919,6 +943,7 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
     for (int i = 0; i < UPL; ++i) ls[i] = iq_lane_scale<FMT>(uk[i], x0[i], x1[i]);
   }
 
+  bool late = false;  // a pairwise wait of this wave ran out (wave-uniform)
   auto finish_tile = [&](std::uint32_t sj, std::uint32_t t, std::uint32_t parity, std::uint32_t gpar,
                          const UnitRaw (&raw)[TILE][UPL]) {
     // Every wave of the workgroup runs the same rounds, so the barrier below is
@@ -969,12 +994,13 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
         // order once all are announced (the same sum as below)
         const std::uint32_t w0 = wave - kw;
         if (kw != 0u) {
-          if (sj >= 2u) pair_wait(&taken[w0], sj - 1u);
+          if (sj >= 2u) late |= !pair_wait(&taken[w0], sj - 1u + epi.wait.bias, epi.wait.limit);
           if ((lane % spread) == 0u) part[parity][wave][r] = v;
           pair_publish(&ready[wave], sj + 1u);
           return;
         }
-        for (std::uint32_t k = 1; k < ks; ++k) pair_wait(&ready[wave + k], sj + 1u);
+        for (std::uint32_t k = 1; k < ks; ++k)
+          late |= !pair_wait(&ready[wave + k], sj + 1u + epi.wait.bias, epi.wait.limit);
         for (std::uint32_t k = 1; k < ks; ++k) v += part[parity][wave + k][r];
         pair_publish(&taken[wave], sj + 1u);
       } else {
@@ -1043,6 +1069,10 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
   }
   if constexpr (EpiHasFinish<Epi>::value) {
     if (kw == 0u) epi.finish(blockIdx.x * nrg + rg, lane);
+  }
+  if constexpr (kPair) {
+    if (late && lane == 0u && epi.wait.status != nullptr)
+      __hip_atomic_fetch_or(epi.wait.status, kStatusWaitTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -38,6 +38,9 @@ _LAUNCH_SIGS: dict[str, list] = {
     "rtxllm_matvec": [c_int, _P, _P, _P, _P, _U, _U, _S],
     "rtxllm_stage_activation": [_P, _P, _U, _P, _S],
     "rtxllm_matvec_xq": [c_int, _P, _P, _P, _P, _U, _U, _S],
+    "rtxllm_matvec_xq_mfma": [c_int, _P, _P, _P, _U, _U, _S],
+    "rtxllm_gate_up_silu": [c_int, _P, _P, _P, _P, _U, c_float, _P, _U, _U, _P, _S],
+    "rtxllm_test_gate_up_silu_waits": [c_int, _P, _P, _P, _P, _U, c_float, _P, _U, _U, _P, _U, _U, _S],
     "rtxllm_stage_batch": [_P, _U, _U, _P, _S],
     "rtxllm_matvec_batch": [c_int, _P, _P, _P, _P, _U, _U, _U, _P, c_size_t, _S],
     "rtxllm_matvec_batch_f32": [c_int, _P, _P, _P, _P, _U, _U, _U, _P, c_size_t, _S],

@@ -17,6 +17,17 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: multi-second CPU oracle runs")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """Greedy tokens that differed from the oracle's at a near-tie (tests/token_rule.py)."""
+    mod = sys.modules.get("token_rule")
+    if mod is None:
+        return
+    rows = mod.DISAGREEMENTS
+    terminalreporter.write_line(f"token disagreements at near-ties: {len(rows)}")
+    for label, tok, ref, gap in rows:
+        terminalreporter.write_line(f"  {label}: token {tok}, oracle {ref}, relative gap {gap:.3e}")
+
+
 @pytest.fixture(scope="session")
 def orc():
     from oracle import binding

@@ -103,12 +103,17 @@ def test_embed_gather_q5k_bit_exact(orc):
         assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), t
 
 
-@pytest.mark.parametrize("heads", [(32, 8), (16, 16), (8, 2)], ids=["gqa4", "mha", "gqa4-small"])
-def test_attn_decode_gqa_f16_matches_oracle(orc, heads):
+@pytest.mark.parametrize("positions", [(0, 130, 2047, 4095), (3001,)], ids=["four-queries", "one-query"])
+@pytest.mark.parametrize("heads", [(32, 8), (16, 16), (8, 2), (64, 8), (16, 8)],
+                         ids=["gqa4", "mha", "gqa4-small", "gqa8", "gqa2"])
+def test_attn_decode_gqa_f16_matches_oracle(orc, heads, positions):
+    """Groups 1, 2, 4 and 8 (group 8 fills all 16 B-operand columns of the
+    score MFMA: 8 heads x hi / lo); several queries run the batch kernels,
+    one query the batch-1 kernels of the decode step."""
     n_heads, n_kv = heads
     hd, page, cap = 128, 64, 4096
     pps = cap // page
-    positions = np.array([0, 130, 2047, 4095], np.uint32)
+    positions = np.array(positions, np.uint32)
     count = len(positions)
     npages = count * pps
     # pages of all queries in one cache, interleaved by a permutation

@@ -15,6 +15,8 @@ from rtxllm_amd import formats as F  # noqa: E402
 from rtxllm_amd import ops, packs  # noqa: E402
 from rtxllm_amd._lib import lib  # noqa: E402
 
+from token_rule import check_token  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3  # max |y_gpu - y_ref| / max |y_ref|, fp32 accumulation
@@ -166,8 +168,8 @@ def check_decode(orc, name, pack, rows_limit=None):
     assert np.max(np.abs(got_kv - ref_kv)) <= TOL * np.max(np.abs(ref_l))
     assert (got_kv != 0).sum() == (ref_kv != 0).sum()
     # a different token only at a near-tie, inside the staging's error (~2e-5 of the maximum)
-    assert got_t == ref_t or abs(float(ref_l[(got_t - token0 - 1) % 32000]) - float(ref_l.max())) <= 1e-4 * abs(
-        float(ref_l.max()))
+    assert ref_t == (int(np.argmax(ref_l)) + token0 + 1) % 32000
+    check_token(f"{name} {pack.rows}x{pack.cols}", (got_t - token0 - 1) % 32000, ref_l, 1e-4)
 
 
 @pytest.mark.parametrize("fmt", list(DECODE_Q4K), ids=lambda f: F.NAMES[f])
