@@ -77,3 +77,44 @@ def gate(label: str, y: np.ndarray, y32: np.ndarray, y64: np.ndarray) -> tuple[f
     assert e_gpu <= GATE * e_f32, (label, "normwise", e_gpu, e_f32)
     assert p_gpu <= GATE * p_f32, (label, "per-element", p_gpu, p_f32)
     return e_gpu, p_gpu
+
+
+def batch_staged(x: np.ndarray) -> np.ndarray:
+    """The activation values the batched matrix-core matvec multiplies: per
+    256-value block, e from max|x| = f 2^e (f in [0.5, 1)), t = x 2^-e in
+    fp32, hi = fp16(t), lo = fp16(t - hi) (round to nearest even, fp16
+    subnormals kept), value (hi + lo) 2^e. Returned as float32, which holds
+    every such value exactly (asserted)."""
+    xb = np.asarray(x, np.float32).reshape(-1, 256)
+    m = np.max(np.abs(xb), axis=1).astype(np.float64)
+    e = np.where((m > 0) & np.isfinite(m), np.frexp(m)[1], 0).astype(np.int64)
+    t = np.ldexp(xb.astype(np.float64), -e[:, None]).astype(np.float32)  # exact: a power-of-two scaling
+    hi = t.astype(np.float16)
+    lo = (t - hi.astype(np.float32)).astype(np.float16)
+    v = np.ldexp(hi.astype(np.float64) + lo.astype(np.float64), e[:, None])
+    out = v.astype(np.float32)
+    assert np.array_equal(out.astype(np.float64), v), "staged value not exact in fp32"
+    return out.reshape(-1)
+
+
+def gate_staged(label: str, y: np.ndarray, y32: np.ndarray, y64: np.ndarray, yst64: np.ndarray) -> tuple[float, float]:
+    """Gate of a kernel that rounds its activation once on input (the batched
+    matrix-core matvec keeps ~22 bits per 256-value block, so a block whose
+    values span many decades loses the small ones' low bits; fp32 keeps 24
+    bits per value). yst64 is the float64 product with the rounded activation.
+      * the kernel's arithmetic on its rounded input: both measures of y
+        against yst64 at most GATE times the fp32-sequential path's against y64;
+      * normwise against y64 at most GATE times the fp32-sequential path's;
+      * per element against y64 at most GATE times the larger of the
+        fp32-sequential path's and the input rounding's own (yst64 against y64).
+    Returns (normwise, per-element) of y against y64."""
+    e_gpu, e_f32 = err64(y, y64), err64(y32, y64)
+    p_gpu, p_f32, p_st = elem64(y, y64), elem64(y32, y64), elem64(yst64, y64)
+    e_ar, p_ar = err64(y, yst64), elem64(y, yst64)
+    print(f"{label}: normwise gpu {e_gpu:.3e} fp32-seq {e_f32:.3e} arith {e_ar:.3e}; per-element (floor {FLOOR:g}) "
+          f"gpu {p_gpu:.3e} fp32-seq {p_f32:.3e} staging {p_st:.3e} arith {p_ar:.3e}")
+    assert e_ar <= GATE * e_f32, (label, "normwise arithmetic", e_ar, e_f32)
+    assert p_ar <= GATE * p_f32, (label, "per-element arithmetic", p_ar, p_f32)
+    assert e_gpu <= GATE * e_f32, (label, "normwise", e_gpu, e_f32)
+    assert p_gpu <= GATE * max(p_f32, p_st), (label, "per-element", p_gpu, p_f32, p_st)
+    return e_gpu, p_gpu

@@ -27,7 +27,7 @@ from rtxllm_amd._lib import lib  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-from precision_ref import GATE, activation, elem64, err64, gate, references  # noqa: E402,F401
+from precision_ref import GATE, activation, batch_staged, elem64, err64, gate, gate_staged, oracle_args, references  # noqa: E402,F401
 
 
 CONFIG_CASES = (
@@ -277,7 +277,9 @@ def test_matvec_batch8_config_shapes(orc, fmt, shape):
                                        rows, cols, 8, ops.ptr(ws) if need else None, need, ops.stream())
     assert rc == 0
     assert np.array_equal(y_self.cpu().numpy().view(np.uint32), y.view(np.uint32))
+    of, pl, mt = oracle_args(pack)
     for s in range(8):
         y32, y64 = references(orc, pack, xs[s])
+        yst64 = orc.matvec_f64(of, pl, mt, batch_staged(xs[s]), rows, cols, 16)
         assert float(np.max(np.abs(y[s] - y32)) / np.max(np.abs(y32))) <= 1e-3
-        gate(f"{F.NAMES[fmt]} {rows}x{cols} seq {s} {kinds[s]}", y[s], y32, y64)
+        gate_staged(f"{F.NAMES[fmt]} {rows}x{cols} seq {s} {kinds[s]}", y[s], y32, y64, yst64)
