@@ -57,9 +57,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--units-sweep", action="store_true",
                     help="time the IQ decode matvecs in the GGUF and the unit layouts (batch 1, HBM-cold)")
     ap.add_argument("--mfma-probe", action="store_true",
-                    help="run the batch-8 matvec stages of one layer (the matrix-core counter workload)")
+                    help="run the batch-1 gate_up and attention and the batch-8 matvec stages of one layer (the "
+                         "matrix-core counter workload)")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
-                    help="matrix-core FLOP and rate per batch matvec kernel from the counter and trace runs")
+                    help="matrix-core work, rate and busy share per matrix-core kernel from the counter and trace runs")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="per-kernel launch statistics of a rocprofv3 --kernel-trace run as a markdown table, "
                          "with the kernels both decode paths launch split by grid size")
@@ -67,6 +68,9 @@ def parse() -> argparse.Namespace:
                     help="instruction accounting per decode stage kernel from rocprofv3 --pmc runs of "
                          "--traffic-probe (SQ_* counters, any split over passes), with the VALU issue floor "
                          "against the time budget at 70%% of the HBM peak")
+    ap.add_argument("--timeline", action="store_true",
+                    help="run the batch-1 step on the profiling build (build/librtxllm_timeline.so) and print the "
+                         "per-wave timeline of its last layer and LM head as markdown, nothing else")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -248,6 +252,8 @@ def decode_bench(torch, args, batch: int = 1) -> dict:
     for v in stages.values():
         v["frac"] = round(v["GB/s"] / HBM_PEAK_GBS, 4)
         v["share_of_step"] = round(v["us"] * v["launches_per_step"] / (ms * 1e3), 4)
+    for st, dist in phase_latency(torch, m, stream, shape.n_layers, min(args.steps, 50)).items():
+        stages[st]["launch_latency"] = dist
     dom = max(stages, key=lambda k: stages[k]["us"] * stages[k]["launches_per_step"])
     launches = m.launches_per_step()
     buckets = None if args.no_context_buckets else context_buckets(torch, m, stream, token, batch, args.steps)
@@ -257,6 +263,39 @@ def decode_bench(torch, args, batch: int = 1) -> dict:
         "GB/s": step_bytes / (ms * 1e-3) / 1e9, "stages": stages, "dominant": dom, "launches": launches,
         "mean_context": mean_ctx, "tokens_after": tokens, "context_buckets": buckets,
     }
+
+
+def phase_latency(torch, m, stream, n_layers: int, steps: int) -> dict:
+    """Per-launch latency distribution of each stage, as the reference times
+    its phases (main.cpp:4838-4907: an event before and after each launch,
+    every launch issued on its own, percentiles over the samples): `steps`
+    passes over the step's stages in order (every layer's qkv, attention, o,
+    gate_up, down, then the LM head), each launch between two events on the
+    launch stream. Launches are issued from the host one by one, so each runs
+    on an otherwise idle GPU: these figures include the launch's own ramp and
+    drain, unlike the graph-replay means."""
+    import numpy as np
+
+    sp = stream.cuda_stream
+    order = [(l, st) for l in range(n_layers) for st in ("qkv", "attention", "o", "gate_up", "down")]
+    order.append((0, "lm_head"))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+    samples: dict = {}
+    with torch.cuda.stream(stream):
+        for _ in range(steps):
+            for (l, st), (e0, e1) in zip(order, evs):
+                e0.record(stream)
+                m.launch_stage(l, st, sp)
+                e1.record(stream)
+            evs[-1][1].synchronize()
+            for (l, st), (e0, e1) in zip(order, evs):
+                samples.setdefault(st, []).append(e0.elapsed_time(e1) * 1e3)
+    out = {}
+    for st, v in samples.items():
+        a = np.array(v)
+        out[st] = {f"p{q}": round(float(np.percentile(a, q)), 3) for q in (50, 95, 99)}
+        out[st].update({"mean": round(float(a.mean()), 3), "samples": int(a.size), "unit": "us per launch"})
+    return out
 
 
 SHORT_POS = 64  # a short context: the first step's position
@@ -328,53 +367,71 @@ MFMA_STAGES = ("qkv", "o", "gate_up", "down", "lm_head")
 
 
 def mfma_probe(torch) -> None:
-    """The workload of the matrix-core counter pass: the batch-8 decode step's
-    matvec stages of layer 0 (8 sequences at ~4030 positions), three times each."""
+    """The workload of the matrix-core counter pass: the batch-1 decode step's
+    gate_up (int8 matrix cores) and attention (fp16 score MFMAs) and the
+    batch-8 step's matvec stages, layer 0 at ~4030 positions, three times each."""
     import dataclasses
 
     from rtxllm_amd.llama import LLAMA_8B
 
-    shape = dataclasses.replace(LLAMA_8B, batch=8)
-    m, token = build_model(torch, shape)
-    m.set_token_pos(token, [shape.max_ctx - 64] * 8)
     sp = torch.cuda.current_stream().cuda_stream
-    for _ in range(3):
-        for st in MFMA_STAGES:
-            m.launch_stage(0, st, sp)
-    torch.cuda.synchronize()
-    m.close()
+    for batch, stages in ((1, ("gate_up", "attention")), (8, MFMA_STAGES)):
+        shape = dataclasses.replace(LLAMA_8B, batch=batch)
+        m, token = build_model(torch, shape)
+        m.set_token_pos(token, [shape.max_ctx - 64] * batch if batch > 1 else shape.max_ctx - 64)
+        for _ in range(3):
+            for st in stages:
+                m.launch_stage(0, st, sp)
+        torch.cuda.synchronize()
+        m.close()
+
+
+MFMA_KERNELS = ("mm_kernel", "mvq_kernel", "attn_partial_kernel")
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_VALU_MFMA_BUSY_CYCLES",
+                 "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE")
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak
 
 
 def mfma_summary(pmc_dir: str, trace_dir: str) -> str:
-    """Per batch matvec kernel: fp16 matrix-core FLOP per dispatch from
-    SQ_INSTS_VALU_MFMA_MOPS_F16 (units of 512 FLOP), the algorithmic FLOP of the
-    8-sequence product (2 rows cols 16: 8 sequences x hi/lo columns), the mean
-    dispatch time from the kernel trace of the same workload, and the achieved
-    rate against the dense fp16 peak."""
+    """Per matrix-core kernel (batch matvecs, the batch-1 gate_up, attention
+    partials): matrix-core work per dispatch from SQ_INSTS_VALU_MFMA_MOPS_F16 /
+    _I8 (units of 512 FLOP or OP), the mean dispatch time from the kernel trace
+    of the same workload, the achieved rate against the dense fp16 / int8 peak,
+    and the matrix-core busy share: SQ_VALU_MFMA_BUSY_CYCLES (summed over the
+    1024 SIMDs) / (1024 * the kernel's busy cycles), where GRBM_GUI_ACTIVE sums
+    the 8 XCDs' busy cycles (busy = GRBM_GUI_ACTIVE / 8)."""
     import csv
     import glob
 
-    mops: dict = {}
+    vals: dict = {}
     for f in glob.glob(str(Path(pmc_dir) / "**" / "*counter_collection.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
-            if r["Counter_Name"] == "SQ_INSTS_VALU_MFMA_MOPS_F16" and "mm_kernel" in r["Kernel_Name"]:
-                mops.setdefault((r["Kernel_Name"], r["Grid_Size"]), []).append(float(r["Counter_Value"]))
+            if r["Counter_Name"] in MFMA_COUNTERS and any(k in r["Kernel_Name"] for k in MFMA_KERNELS):
+                key = (r["Kernel_Name"], r["Grid_Size"])
+                vals.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     dur: dict = {}
     for f in glob.glob(str(Path(trace_dir) / "**" / "*kernel_trace.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
-            if "mm_kernel" in r["Kernel_Name"]:
+            if any(k in r["Kernel_Name"] for k in MFMA_KERNELS):
                 g = str(int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
                 us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
                 dur.setdefault((r["Kernel_Name"], g), []).append(us)
+    mean = lambda v: sum(v) / len(v) if v else float("nan")
     lines = []
-    for (name, grid), v in sorted(mops.items(), key=lambda kv: kv[0]):
-        flop = 512.0 * sum(v) / len(v)
-        d = dur.get((name, grid))
-        us = sum(d) / len(d) if d else float("nan")
-        short = name.replace("rtxllm::(anonymous namespace)::", "").replace("rtxllm::", "").replace("void ", "")
-        short = short.split("(")[0]
-        lines.append(f"{short} grid {grid}: mfma_flop {flop:.4g} us {us:.2f} TFLOP/s {flop / us / 1e6:.2f} "
-                     f"frac_of_fp16_peak {flop / us / 1e6 / MFMA_PEAK_TFLOPS:.5f}")
+    for (name, grid), c in sorted(vals.items(), key=lambda kv: kv[0]):
+        f16 = 512.0 * mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", []))
+        i8 = 512.0 * mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", []))
+        busy, gui = mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [])), mean(c.get("GRBM_GUI_ACTIVE", []))
+        us = mean(dur.get((name, grid), []))
+        short = _short_kernel(name)
+        line = f"{short} grid {grid}: us {us:.2f}"
+        if f16 > 0:
+            line += f" f16_flop {f16:.4g} TFLOP/s {f16 / us / 1e6:.2f} frac_of_fp16_peak {f16 / us / 1e6 / MFMA_PEAK_TFLOPS:.5f}"
+        if i8 > 0:
+            line += f" i8_op {i8:.4g} TOP/s {i8 / us / 1e6:.2f} frac_of_int8_peak {i8 / us / 1e6 / INT8_PEAK_TOPS:.5f}"
+        if busy == busy and gui == gui and gui > 0:
+            line += f" mfma_busy_cycles {busy:.4g} gui_active {gui:.4g} mfma_busy_share {busy * 8 / (gui * 1024):.4f}"
+        lines.append(line)
     return "\n".join(lines) + "\n"
 
 
@@ -412,6 +469,94 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> str:
         wb = write.get(k, 0.0) * 1024.0 * w_scale
         lines.append(f"{st} fetch_bytes {fb:.0f} write_bytes {wb:.0f} traffic_bytes {fb + wb:.0f}")
     return "\n".join(lines) + "\n"
+
+
+TL_REGION = 65536  # slots per timeline region (csrc/timeline.h)
+TL_US = 0.01        # s_memrealtime counts (100 MHz)
+
+
+def timeline(torch) -> str:
+    """Per-wave timeline of one batch-1 decode step (8B shapes, context ~4050)
+    from the profiling build: each kernel role's stamps describe its last
+    launch in the step (layer 31, then the LM head). Three replays, each
+    summarised; times in us from the first qkv wave's entry."""
+    import numpy as np
+
+    from rtxllm_amd import _lib
+
+    _lib.LIB_PATH = _lib.LIB_PATH.with_name("librtxllm_timeline.so")
+    import ctypes
+
+    from rtxllm_amd.llama import LLAMA_8B
+
+    L = _lib.lib()
+    L.rtxllm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    m, token = build_model(torch, LLAMA_8B)
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    m.set_token_pos(token, LLAMA_8B.max_ctx - 40)
+    m.graph_capture(sp)
+    for _ in range(10):
+        m.graph_replay(sp)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            m.graph_replay(sp)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / 20
+    out = [f"instrumented step: {step_ms:.4f} ms (mean of 20 graph replays)", "",
+           "| replay | stage | waves | first entry | last entry | first end | median end | last end | gap before |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    notes = []
+    for rep in range(3):
+        assert L.rtxllm_timeline_clear() == 0
+        torch.cuda.synchronize()
+        m.graph_replay(sp)
+        torch.cuda.synchronize()
+        b = np.zeros(8 * TL_REGION, np.uint64)
+        assert L.rtxllm_timeline_read(b.ctypes.data, b.size) == 0
+        b = b.astype(np.int64)
+        t0 = b[b > 0].min()
+        reg = lambda r, k: b[r * TL_REGION:(r + 1) * TL_REGION].reshape(-1, k)
+        roles = [("qkv", reg(3, 2), 0, 1), ("attention partial", reg(0, 4), 0, 3), ("attention combine", reg(1, 4), 0, 2),
+                 ("o", reg(4, 2), 0, 1), ("gate_up", reg(2, 8), 0, 7), ("down", reg(5, 2), 0, 1),
+                 ("LM head", reg(6, 2), 0, 1)]
+        prev_end = None
+        for name, a, pe, pd in roles:
+            a = a[a[:, pe] > 0]
+            ent, end = (a[:, pe] - t0) * TL_US, (a[:, pd] - t0) * TL_US
+            gap = "" if prev_end is None else f"{ent.min() - prev_end:.2f}"
+            out.append(f"| {rep} | {name} | {a.shape[0]} | {ent.min():.2f} | {ent.max():.2f} | {end.min():.2f} | "
+                       f"{np.median(end):.2f} | {end.max():.2f} | {gap} |")
+            prev_end = end.max()
+        p = reg(0, 4)
+        p = p[(p[:, 0] > 0) & (p[:, 1] > 0)]
+        c = reg(1, 4)
+        c = c[c[:, 0] > 0]
+        g = reg(2, 8)
+        g = g[g[:, 0] > 0]
+        med = lambda v: float(np.median(v)) * TL_US
+        notes.append(f"- replay {rep}: attention partial per wave: entry to scores {med(p[:, 1] - p[:, 0]):.2f} "
+                     f"(p90 {np.percentile(p[:, 1] - p[:, 0], 90) * TL_US:.2f}), scores to weighted V sum "
+                     f"{med(p[:, 2] - p[:, 1]):.2f}, to end (record merge, store) {med(p[:, 3] - p[:, 2]):.2f}; "
+                     f"combine per wave: entry to merged {med(c[:, 1] - c[:, 0]):.2f}, staging {med(c[:, 2] - c[:, 1]):.2f}; "
+                     f"gate_up per wave: entry to codebook barrier {med(g[:, 1] - g[:, 0]):.2f}, rounds "
+                     + ", ".join(f"{med(g[g[:, k + 1] > 0, k + 1] - g[g[:, k + 1] > 0, k]):.2f}" for k in range(1, 5)
+                                 if (g[:, k + 1] > 0).any()))
+        lm = reg(6, 2)
+        slots = np.nonzero(lm[:, 0] > 0)[0]
+        wg = slots // 8  # the logits epilogue's slot stride: 8 waves per workgroup
+        end = (lm[slots, 1] - t0) * TL_US
+        rank = wg // 8   # dispatch rank of the workgroup on its XCD (workgroups go round-robin over 8 XCDs)
+        per = max(1, (int(rank.max()) + 1) // 3)
+        notes.append(f"  LM head wave ends by dispatch rank within the XCD: " + ", ".join(
+            f"ranks {lo}-{lo + per - 1} median {float(np.median(end[(rank >= lo) & (rank < lo + per)])):.2f}"
+            for lo in range(0, int(rank.max()) + 1, per)))
+    m.close()
+    return "\n".join(out) + "\n\n" + "\n".join(notes) + "\n"
 
 
 def _short_kernel(name: str) -> str:
@@ -820,6 +965,9 @@ def main() -> int:
         return 0
     if args.mfma_probe:
         mfma_probe(torch)
+        return 0
+    if args.timeline:
+        sys.stdout.write(timeline(torch))
         return 0
     if args.read_ceiling:
         print(json.dumps({"read_ceiling": read_ceiling(torch)}), flush=True)

@@ -100,6 +100,7 @@ __device__ __forceinline__ void stage_group16(const XQOut& xq, std::uint32_t g0,
 // ---- epilogues (TILE 4: row r of a tile in lanes [16 r, 16 r + 16)) ---------
 
 struct EpiQkv {
+  static constexpr int tl_region(int) { return kTlQkv; }
   static constexpr int kTile = 4;
   const float* sumsq;
   std::uint32_t nslots, n;
@@ -174,6 +175,7 @@ struct EpiGateUpWide : EpiGateUp {
 // in a register and stores it once, after its last tile, into its own slot;
 // the finalize kernel reduces the slots (no atomics, no per-tile reads).
 struct EpiLogits {
+  static constexpr int tl_region(int) { return kTlLogits; }
   static constexpr int kTile = 4;
   static constexpr bool kFinish = true;
   const float* sumsq;
@@ -209,6 +211,7 @@ struct EpiLogits {
 // Residual add and next-norm staging over 16-row groups (one staged group of
 // the next matvec's input): lane i < 16 of wave 0 owns row row0 + i.
 struct EpiResidual {
+  static constexpr int tl_region(int fmt) { return fmt_is_iq(fmt) ? kTlResidualIq : kTlResidualK; }
   static constexpr int kTile = 4;
   static constexpr std::uint32_t kGroupRows = kXGroup;
   float* h;
@@ -332,6 +335,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
   const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
+  const int tl_r = gridDim.z == 1u ? kTlAttnPartial : -1;
+  const std::uint32_t tl_slot = ((blockIdx.y * gridDim.x + blockIdx.x) * kAttnWaves + (threadIdx.x >> 6)) * 4u;
+  tl_stamp(tl_r, tl_slot);
   const std::uint32_t seq = blockIdx.z;
   q += static_cast<std::size_t>(seq) * q_stride;
   partials += static_cast<std::size_t>(seq) * part_stride;
@@ -361,6 +367,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
   if (p0 > pos) {  // chunk beyond the context (uniform over the workgroup): empty record
     for (std::uint32_t i = threadIdx.x; i < GROUP * (kHeadDim + 2u); i += blockDim.x)
       rec[i] = (i % (kHeadDim + 2u)) == 0u ? -INFINITY : 0.0f;
+    tl_stamp(tl_r, tl_slot + 3u);
     return;
   }
   // K / V row offset (elements; the host checks that a layer's cache has fewer
@@ -410,6 +417,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
   }
   l += lane_xor<16>(l);
   l += lane_xor<32>(l);
+  tl_stamp(tl_r, tl_slot + 1u);
   float o0[GROUP], o1[GROUP];
 #pragma unroll
   for (int h = 0; h < GROUP; ++h) o0[h] = o1[h] = 0.0f;
@@ -432,9 +440,13 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
     wrec[wave][lane >> 1][0] = m;
     wrec[wave][lane >> 1][1] = l;
   }
+  tl_stamp(tl_r, tl_slot + 2u);
   __syncthreads();
   // wave h merges head h's records
-  if (wave >= static_cast<std::uint32_t>(GROUP)) return;
+  if (wave >= static_cast<std::uint32_t>(GROUP)) {
+    tl_stamp(tl_r, tl_slot + 3u);
+    return;
+  }
   {
     const std::uint32_t h = wave;
     float M = wrec[0][h][0];  // finite: wave 0 holds position p0
@@ -456,6 +468,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
       rr[1] = L;
     }
   }
+  tl_stamp(tl_r, tl_slot + 3u);
 }
 
 constexpr std::uint32_t kCombinePass = 32;  // chunk records per combine pass
@@ -514,7 +527,10 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const std::uint32_t head = blockIdx.x, lane = threadIdx.x;
   partials += static_cast<std::size_t>(blockIdx.y) * part_stride;
   att += static_cast<std::size_t>(blockIdx.y) * gridDim.x * kHeadDim;
+  const int tl_r = gridDim.y == 1u ? kTlAttnCombine : -1;
+  tl_stamp(tl_r, head * 4u);
   const float2 a = combine_head(partials, group, nchunks, head, lane);
+  tl_stamp(tl_r, head * 4u + 1u);
   const float a0 = a.x, a1 = a.y;
   const std::uint32_t d0 = head * kHeadDim + 2u * lane;
   *reinterpret_cast<float2*>(att + d0) = make_float2(a0, a1);
@@ -548,6 +564,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     xq.s[t] = sc.s;
     xq.sum[t] = sc.s * static_cast<float>(total);
   }
+  tl_stamp(tl_r, head * 4u + 2u);
 }
 
 // Batch form with the o projection's staging fused: wave w of workgroup
@@ -831,3 +848,21 @@ hipError_t launch_synth_q4k_native(std::uint64_t seed, std::size_t n_blocks, flo
 }
 
 }  // namespace rtxllm
+
+#ifdef RTXLLM_TIMELINE
+#include "rtxllm/timeline.h"
+
+extern "C" hipError_t rtxllm_timeline_read(unsigned long long* host, size_t count) {
+  if (host == nullptr || count > static_cast<size_t>(rtxllm::kTlRegions) * rtxllm::kTlRegion)
+    return hipErrorInvalidValue;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(rtxllm::g_timeline), count * sizeof(unsigned long long), 0,
+                             hipMemcpyDeviceToHost);
+}
+
+extern "C" hipError_t rtxllm_timeline_clear(void) {
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(rtxllm::g_timeline));
+  if (e != hipSuccess) return e;
+  return hipMemset(p, 0, sizeof(rtxllm::g_timeline));
+}
+#endif

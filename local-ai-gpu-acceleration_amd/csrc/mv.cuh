@@ -24,6 +24,7 @@
 
 #include "common.h"
 #include "iq_grids.h"
+#include "timeline.h"
 #include "xq.h"
 
 namespace rtxllm {
@@ -768,6 +769,9 @@ template <int FMT, int UPL, int TILE, bool SELF, class Epi>
 __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w, XSrc xs, std::uint32_t rows,
                                                                       std::uint32_t ks, Epi epi_arg) {
   static_assert(Epi::kTile == TILE, "epilogue tile");
+  constexpr int kTlR = TlRegionOf<Epi>::value(FMT);
+  const std::uint32_t tl_slot = (blockIdx.x * EpiWaves<Epi>::value + (threadIdx.x >> 6)) * 2u;
+  tl_stamp(kTlR, tl_slot);
   constexpr std::uint32_t GR = EpiGroupRows<Epi>::value;
   static_assert(GR % TILE == 0u, "epilogue group of whole tiles");
   constexpr std::uint32_t TG = GR > 0u ? GR / TILE : 1u;  // tiles per group
@@ -1074,6 +1078,7 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
     if (late && lane == 0u && epi.wait.status != nullptr)
       __hip_atomic_fetch_or(epi.wait.status, kStatusWaitTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  tl_stamp(kTlR, tl_slot + 1u);
 }
 
 // ---- epilogues ---------------------------------------------------------------

@@ -127,6 +127,8 @@ __global__ __launch_bounds__(64 * kMqMaxWaves) void mvq_kernel(QTensor w, XQ xq,
   static_assert(Epi::kTile == 4, "epilogue tile of 4 rows");
   static_assert(EpiGroupRows<Epi>::value == 0u && !EpiHasFinish<Epi>::value, "plain epilogues");
   Epi epi = epi_arg;
+  const std::uint32_t tl_slot = (blockIdx.x * kMqMaxWaves + (threadIdx.x >> 6)) * 8u;
+  tl_stamp(kTlGateUpMq, tl_slot);
   __shared__ float part[2][kMqMaxWaves][kMqRows];
   const std::uint32_t lane = threadIdx.x & 63u;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -186,6 +188,7 @@ __global__ __launch_bounds__(64 * kMqMaxWaves) void mvq_kernel(QTensor w, XQ xq,
     reinterpret_cast<std::uint32_t*>(xw + 1664u)[lane & 31u] = 0u;
   }
   lds_grid_commit(tables, grid_stage, iq_image<FMT>(), threadIdx.x, blockDim.x);
+  tl_stamp(kTlGateUpMq, tl_slot + 1u);
   if constexpr (EpiHasReady<Epi>::value) epi.ready(lane);
   // A operand: lane (m = lane & 15, s = lane >> 4) holds digit m & 3 of the
   // group of unit i, half h, of slice s when m >> 2 == s and m & 3 < 3, else
@@ -270,6 +273,7 @@ __global__ __launch_bounds__(64 * kMqMaxWaves) void mvq_kernel(QTensor w, XQ xq,
       for (std::uint32_t k = 1; k < nw; ++k) y += part[par][k][rr];
       epi(t * kMqRows + 4u * j, y, lane, rows);
     }
+    tl_stamp(kTlGateUpMq, tl_slot + 2u + (s < 4u ? s : 4u));
   };
 
   // Round s computes buf[s % 2] after requesting round s + 1 (no load inside
@@ -288,6 +292,7 @@ __global__ __launch_bounds__(64 * kMqMaxWaves) void mvq_kernel(QTensor w, XQ xq,
   } else {
     round(s, buf[0]);
   }
+  tl_stamp(kTlGateUpMq, tl_slot + 7u);
 }
 
 // Whether mvq_kernel takes a matvec: a unit layout, whole 16-row tiles and

@@ -15,9 +15,15 @@ from rtxllm_amd import packs
 REPO = Path(__file__).resolve().parent.parent
 
 
-def declared_functions() -> list[str]:
+# entry points of the profiling build (build/librtxllm_timeline.so) only
+PROFILING_HEADERS = ("timeline.h",)
+
+
+def declared_functions(profiling: bool = False) -> list[str]:
     names = []
     for hdr in sorted((REPO / "include" / "rtxllm").glob("*.h")):
+        if (hdr.name in PROFILING_HEADERS) != profiling:
+            continue
         text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
         names += re.findall(r"^\s*(?:hipError_t|int|uint32_t|size_t|void\s*\*|void)\s*(rtxllm_\w+)\s*\(", text,
                             flags=re.M)
@@ -29,6 +35,23 @@ def test_library_exports_every_declared_symbol(rlib):
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(rlib, n)]
     assert not missing, missing
+
+
+def test_profiling_build_exports_the_library_and_its_timeline():
+    """build/librtxllm_timeline.so is the library plus the timeline entry
+    points; the library proper does not export them."""
+    import ctypes
+
+    from rtxllm_amd import _lib
+
+    prof = declared_functions(profiling=True)
+    assert prof == ["rtxllm_timeline_read", "rtxllm_timeline_clear"]
+    path = _lib.LIB_PATH.with_name("librtxllm_timeline.so")
+    assert path.is_file(), path
+    tl = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
+    missing = [n for n in declared_functions() + prof if not hasattr(tl, n)]
+    assert not missing, missing
+    assert not any(hasattr(_lib.lib(), n) for n in prof)
 
 
 def test_measurement_probe_is_not_in_the_library(rlib):
