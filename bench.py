@@ -69,8 +69,8 @@ def parse() -> argparse.Namespace:
                          "--traffic-probe (SQ_* counters, any split over passes), with the VALU issue floor "
                          "against the time budget at 70%% of the HBM peak")
     ap.add_argument("--timeline", action="store_true",
-                    help="run the batch-1 step on the profiling build (build/librtxllm_timeline.so) and print the "
-                         "per-wave timeline of its last layer and LM head as markdown, nothing else")
+                    help="run the batch-1 and batch-8 steps on the profiling build (build/librtxllm_timeline.so) and "
+                         "print the per-wave timeline of their last layer and LM head as markdown, nothing else")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of --traffic-probe (FETCH_SIZE, WRITE_SIZE) as "
                          "HBM bytes per launch, calibrated on the copy kernel")
@@ -472,29 +472,25 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> str:
 
 
 TL_REGION = 65536  # slots per timeline region (csrc/timeline.h)
-TL_US = 0.01        # s_memrealtime counts (100 MHz)
+TL_REGIONS = 32    # 16 per instrumented translation unit (layer.hip, batch.hip)
+TL_US = 0.01       # s_memrealtime counts (100 MHz)
 
 
-def timeline(torch) -> str:
-    """Per-wave timeline of one batch-1 decode step (8B shapes, context ~4050)
-    from the profiling build: each kernel role's stamps describe its last
-    launch in the step (layer 31, then the LM head). Three replays, each
-    summarised; times in us from the first qkv wave's entry."""
+def _timeline_step(torch, L, batch: int):
+    """Builds the 8B-shape model at `batch`, replays its step graph and yields
+    (instrumented step ms, [record of each of three further replays])."""
+    import dataclasses
+
     import numpy as np
-
-    from rtxllm_amd import _lib
-
-    _lib.LIB_PATH = _lib.LIB_PATH.with_name("librtxllm_timeline.so")
-    import ctypes
 
     from rtxllm_amd.llama import LLAMA_8B
 
-    L = _lib.lib()
-    L.rtxllm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
-    m, token = build_model(torch, LLAMA_8B)
+    shape = dataclasses.replace(LLAMA_8B, batch=batch)
+    m, token = build_model(torch, shape)
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
-    m.set_token_pos(token, LLAMA_8B.max_ctx - 40)
+    p0 = shape.max_ctx - 40
+    m.set_token_pos(token, [p0] * batch if batch > 1 else p0)
     m.graph_capture(sp)
     for _ in range(10):
         m.graph_replay(sp)
@@ -507,56 +503,114 @@ def timeline(torch) -> str:
         e1.record(stream)
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / 20
-    out = [f"instrumented step: {step_ms:.4f} ms (mean of 20 graph replays)", "",
-           "| replay | stage | waves | first entry | last entry | first end | median end | last end | gap before |",
-           "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
-    notes = []
-    for rep in range(3):
+    records = []
+    for _ in range(3):
         assert L.rtxllm_timeline_clear() == 0
         torch.cuda.synchronize()
         m.graph_replay(sp)
         torch.cuda.synchronize()
-        b = np.zeros(8 * TL_REGION, np.uint64)
+        b = np.zeros(TL_REGIONS * TL_REGION, np.uint64)
         assert L.rtxllm_timeline_read(b.ctypes.data, b.size) == 0
-        b = b.astype(np.int64)
-        t0 = b[b > 0].min()
-        reg = lambda r, k: b[r * TL_REGION:(r + 1) * TL_REGION].reshape(-1, k)
-        roles = [("qkv", reg(3, 2), 0, 1), ("attention partial", reg(0, 4), 0, 3), ("attention combine", reg(1, 4), 0, 2),
-                 ("o", reg(4, 2), 0, 1), ("gate_up", reg(2, 8), 0, 7), ("down", reg(5, 2), 0, 1),
-                 ("LM head", reg(6, 2), 0, 1)]
+        records.append(b.astype(np.int64))
+    m.close()
+    return step_ms, records
+
+
+def _timeline_table(records, roles) -> list:
+    """Rows of the kernel-span table: roles = [(name, region, points per wave,
+    entry point, end point)]."""
+    import numpy as np
+
+    out = ["| replay | stage | waves | first entry | last entry | first end | median end | last end | gap before |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for rep, b in enumerate(records):
+        t0 = None
         prev_end = None
-        for name, a, pe, pd in roles:
-            a = a[a[:, pe] > 0]
+        for name, r, k, pe, pd in roles:
+            a = b[r * TL_REGION:(r + 1) * TL_REGION].reshape(-1, k)
+            a = a[(a[:, pe] > 0) & (a[:, pd] > 0)]
+            if t0 is None:
+                t0 = a[:, pe].min()
             ent, end = (a[:, pe] - t0) * TL_US, (a[:, pd] - t0) * TL_US
             gap = "" if prev_end is None else f"{ent.min() - prev_end:.2f}"
             out.append(f"| {rep} | {name} | {a.shape[0]} | {ent.min():.2f} | {ent.max():.2f} | {end.min():.2f} | "
                        f"{np.median(end):.2f} | {end.max():.2f} | {gap} |")
             prev_end = end.max()
-        p = reg(0, 4)
+    return out
+
+
+def timeline(torch) -> str:
+    """Per-wave timeline of one decode step (8B shapes, context ~4050) at
+    batch 1 and batch 8, from the profiling build: each kernel role's stamps
+    describe its last launch in the step (layer 31, then the LM head). Three
+    replays each; times in us from the first wave of the layer's first kernel."""
+    import ctypes
+
+    import numpy as np
+
+    from rtxllm_amd import _lib
+
+    _lib.LIB_PATH = _lib.LIB_PATH.with_name("librtxllm_timeline.so")
+    L = _lib.lib()
+    L.rtxllm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    med = lambda v: float(np.median(v)) * TL_US
+    reg = lambda b, r, k: b[r * TL_REGION:(r + 1) * TL_REGION].reshape(-1, k)
+
+    step_ms, records = _timeline_step(torch, L, 1)
+    out = ["## Batch 1", "", f"instrumented step: {step_ms:.4f} ms (mean of 20 graph replays)", ""]
+    out += _timeline_table(records, [("qkv", 3, 2, 0, 1), ("attention partial", 0, 4, 0, 3),
+                                     ("attention combine", 1, 4, 0, 2), ("o", 4, 2, 0, 1), ("gate_up", 2, 8, 0, 7),
+                                     ("down", 5, 2, 0, 1), ("LM head", 6, 2, 0, 1)])
+    out.append("")
+    for rep, b in enumerate(records):
+        p = reg(b, 0, 4)
         p = p[(p[:, 0] > 0) & (p[:, 1] > 0)]
-        c = reg(1, 4)
+        c = reg(b, 1, 4)
         c = c[c[:, 0] > 0]
-        g = reg(2, 8)
+        g = reg(b, 2, 8)
         g = g[g[:, 0] > 0]
-        med = lambda v: float(np.median(v)) * TL_US
-        notes.append(f"- replay {rep}: attention partial per wave: entry to scores {med(p[:, 1] - p[:, 0]):.2f} "
-                     f"(p90 {np.percentile(p[:, 1] - p[:, 0], 90) * TL_US:.2f}), scores to weighted V sum "
-                     f"{med(p[:, 2] - p[:, 1]):.2f}, to end (record merge, store) {med(p[:, 3] - p[:, 2]):.2f}; "
-                     f"combine per wave: entry to merged {med(c[:, 1] - c[:, 0]):.2f}, staging {med(c[:, 2] - c[:, 1]):.2f}; "
-                     f"gate_up per wave: entry to codebook barrier {med(g[:, 1] - g[:, 0]):.2f}, rounds "
-                     + ", ".join(f"{med(g[g[:, k + 1] > 0, k + 1] - g[g[:, k + 1] > 0, k]):.2f}" for k in range(1, 5)
-                                 if (g[:, k + 1] > 0).any()))
-        lm = reg(6, 2)
+        out.append(f"- replay {rep}: attention partial per wave: entry to scores {med(p[:, 1] - p[:, 0]):.2f} "
+                   f"(p90 {np.percentile(p[:, 1] - p[:, 0], 90) * TL_US:.2f}), scores to weighted V sum "
+                   f"{med(p[:, 2] - p[:, 1]):.2f}, to end (record merge, store) {med(p[:, 3] - p[:, 2]):.2f}; "
+                   f"combine per wave: entry to merged {med(c[:, 1] - c[:, 0]):.2f}, staging {med(c[:, 2] - c[:, 1]):.2f}; "
+                   f"gate_up per wave: entry to codebook barrier {med(g[:, 1] - g[:, 0]):.2f}, rounds "
+                   + ", ".join(f"{med(g[g[:, k + 1] > 0, k + 1] - g[g[:, k + 1] > 0, k]):.2f}" for k in range(1, 5)
+                               if (g[:, k + 1] > 0).any()))
+        lm = reg(b, 6, 2)
         slots = np.nonzero(lm[:, 0] > 0)[0]
+        t0 = reg(b, 3, 2)[:, 0]
+        t0 = t0[t0 > 0].min()
         wg = slots // 8  # the logits epilogue's slot stride: 8 waves per workgroup
         end = (lm[slots, 1] - t0) * TL_US
         rank = wg // 8   # dispatch rank of the workgroup on its XCD (workgroups go round-robin over 8 XCDs)
         per = max(1, (int(rank.max()) + 1) // 3)
-        notes.append(f"  LM head wave ends by dispatch rank within the XCD: " + ", ".join(
+        out.append("  LM head wave ends by dispatch rank within the XCD: " + ", ".join(
             f"ranks {lo}-{lo + per - 1} median {float(np.median(end[(rank >= lo) & (rank < lo + per)])):.2f}"
             for lo in range(0, int(rank.max()) + 1, per)))
-    m.close()
-    return "\n".join(out) + "\n\n" + "\n".join(notes) + "\n"
+
+    step_ms, records = _timeline_step(torch, L, 8)
+    out += ["", "## Batch 8", "", f"instrumented step: {step_ms:.4f} ms (mean of 20 graph replays)", ""]
+    out += _timeline_table(records, [("qkv", 16, 16, 0, 15), ("attention partial", 7, 4, 0, 3),
+                                     ("attention combine + staging", 8, 2, 0, 1), ("o", 17, 16, 0, 15),
+                                     ("residual + norm staging", 21, 2, 0, 1), ("gate_up", 18, 16, 0, 15),
+                                     ("down", 19, 16, 0, 15), ("residual + norm staging", 22, 2, 0, 1),
+                                     ("LM head", 20, 16, 0, 15)])
+    out.append("")
+    for rep, b in enumerate(records):
+        parts = []
+        for name, r in (("qkv", 16), ("o", 17), ("gate_up", 18), ("down", 19), ("LM head", 20)):
+            a = reg(b, r, 16)
+            a = a[(a[:, 0] > 0) & (a[:, 1] > 0) & (a[:, 2] > 0)]
+            tiles = [f"{med(a[a[:, k + 1] > 0, k + 1] - a[a[:, k + 1] > 0, k]):.2f}" for k in range(2, 14)
+                     if (a[:, k + 1] > 0).any()]
+            parts.append(f"{name}: entry to codebook barrier {med(a[:, 1] - a[:, 0]):.2f}, to RMSNorm scale "
+                         f"{med(a[:, 2] - a[:, 1]):.2f}, tiles " + ", ".join(tiles))
+        p = reg(b, 7, 4)
+        p = p[(p[:, 0] > 0) & (p[:, 1] > 0)]
+        parts.append(f"attention partial: entry to scores {med(p[:, 1] - p[:, 0]):.2f}, to weighted V sum "
+                     f"{med(p[:, 2] - p[:, 1]):.2f}, to end {med(p[:, 3] - p[:, 2]):.2f}")
+        out.append(f"- replay {rep} per wave (medians): " + "; ".join(parts))
+    return "\n".join(out) + "\n"
 
 
 def _short_kernel(name: str) -> str:

@@ -4,10 +4,10 @@
  * Nsight's; they are for bench.py --timeline and similar tools.
  *
  * The profiling build records s_memrealtime (100 MHz, 10 ns per count, one
- * clock for every CU) per wave at fixed points of the batch-1 step's kernels
- * into a device array of 8 regions x 65536 slots; a launch overwrites the
- * slots of its kernel role, so after one step the array describes the last
- * layer (region and slot layout: csrc/timeline.h). */
+ * clock for every CU) per wave at fixed points of the decode step's kernels
+ * (batch 1 and the batch launches) into 32 regions x 65536 slots; a launch
+ * overwrites the slots of its kernel role, so after one step the array
+ * describes the last layer (region and slot layout: csrc/timeline.h). */
 #ifndef RTXLLM_TIMELINE_H
 #define RTXLLM_TIMELINE_H
 
@@ -18,8 +18,8 @@
 extern "C" {
 #endif
 
-/* Copies the first count entries (at most 8 * 65536) to host memory; waits
- * for the device copy (not capture-safe). */
+/* Copies the whole record, count = 32 * 65536 entries, to host memory; waits
+ * for the device copies (not capture-safe). */
 hipError_t rtxllm_timeline_read(unsigned long long* host, size_t count);
 /* Zeroes every slot (synchronous). */
 hipError_t rtxllm_timeline_clear(void);

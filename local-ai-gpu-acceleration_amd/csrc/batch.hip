@@ -96,6 +96,9 @@ struct RmsStageArgs {
 __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStageArgs a) {
   __shared__ float part[kStageThreads / 64u];
   const std::uint32_t b = blockIdx.x, s = blockIdx.y, c = 256u * b + threadIdx.x, cols = a.cols;
+  const int tl_r = a.res != nullptr && a.groups == 1u ? kTlRmsStageO : kTlRmsStageOther;
+  const std::uint32_t tl_slot = ((s * gridDim.x + b) * (kStageThreads / 64u) + (threadIdx.x >> 6)) * 2u;
+  tl_stamp(tl_r, tl_slot);
   if (b == 0u && s == 0u && threadIdx.x == 0u) *x16_tail(a.x16, cols).eps = a.eps;
   if (s >= a.batch) {
     stage_block_zero(s, b, c, cols, a.x16);
@@ -129,6 +132,7 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
   const float ss = block_reduce(x * x, part, false);
   if (threadIdx.x == 0u) x16_tail(a.x16, cols).ss[s * (cols / 256u) + b] = ss;
   stage_block_value(a.w != nullptr ? x * wmul : x, s, b, c, cols, a.x16, part);
+  tl_stamp(tl_r, tl_slot + 1u);
 }
 
 // ---- batch epilogues --------------------------------------------------------
@@ -137,6 +141,7 @@ __global__ __launch_bounds__(kStageThreads) void rms_stage_batch_kernel(RmsStage
 // k (pairs of adjacent rows), q -> q[s], k and v -> the fp16 cache slot of
 // (sequence s, its position); the rule of the batch-1 qkv epilogue.
 struct MmQkv {
+  static constexpr int tl_region(int) { return kTlMmQkv; }
   std::uint32_t q_rows, kv_rows, batch, table_stride, rope_positions, group;
   const float2* rope;
   const std::uint32_t* pos_ptr;
@@ -167,6 +172,7 @@ struct MmQkv {
 
 // Interleaved gate / up rows: act[s][i] = silu(gate_i) * up_i.
 struct MmGateUp {
+  static constexpr int tl_region(int) { return kTlMmGateUp; }
   float* act;
   std::uint32_t stride;
   __device__ __forceinline__ void init(std::uint32_t) {}
@@ -181,6 +187,7 @@ struct MmGateUp {
 // A thread keeps the best key of its rows; lanes 8 s .. 8 s + 3 of a wave are
 // sequence s's.
 struct MmLogits {
+  static constexpr int tl_region(int) { return kTlMmLogits; }
   float* logits;
   std::uint32_t stride, batch;
   unsigned long long* keys;
@@ -501,3 +508,17 @@ extern "C" hipError_t rtxllm_matvec_batch_f32(int format, const uint8_t* payload
   if (x == nullptr) return hipErrorInvalidValue;
   return matvec_batch(format, payload, meta, x, true, y, rows, cols, batch, workspace, workspace_bytes, stream);
 }
+
+#ifdef RTXLLM_TIMELINE
+namespace rtxllm {
+hipError_t timeline_read_batch(unsigned long long* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), sizeof(g_timeline), 0, hipMemcpyDeviceToHost);
+}
+hipError_t timeline_clear_batch() {
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_timeline));
+  if (e != hipSuccess) return e;
+  return hipMemset(p, 0, sizeof(g_timeline));
+}
+}  // namespace rtxllm
+#endif

@@ -335,8 +335,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_partial_kernel(const _Fl
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   __shared__ float wrec[kAttnWaves][GROUP][kHeadDim + 2u];
   const std::uint32_t c = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63u;
-  const int tl_r = gridDim.z == 1u ? kTlAttnPartial : -1;
-  const std::uint32_t tl_slot = ((blockIdx.y * gridDim.x + blockIdx.x) * kAttnWaves + (threadIdx.x >> 6)) * 4u;
+  const int tl_r = gridDim.z == 1u ? kTlAttnPartial : kTlAttnPartialB;
+  const std::uint32_t tl_slot =
+      (((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kAttnWaves + (threadIdx.x >> 6)) * 4u;
   tl_stamp(tl_r, tl_slot);
   const std::uint32_t seq = blockIdx.z;
   q += static_cast<std::size_t>(seq) * q_stride;
@@ -581,6 +582,8 @@ __global__ __launch_bounds__(128) void attn_combine_x16_kernel(const float* __re
   const std::uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const std::uint32_t b = blockIdx.x, s = blockIdx.y, head = 2u * b + wave;
   const std::uint32_t cols = 2u * gridDim.x * kHeadDim, c0 = head * kHeadDim + 2u * lane;
+  const std::uint32_t tl_slot = ((s * gridDim.x + b) * 2u + wave) * 2u;
+  tl_stamp(kTlCombineB, tl_slot);
   const X16Tail tail = x16_tail(x16, cols);
   if (b == 0u && s == 0u && threadIdx.x == 0u) *tail.eps = -1.0f;
   if (s >= batch) {
@@ -612,6 +615,7 @@ __global__ __launch_bounds__(128) void attn_combine_x16_kernel(const float* __re
     x16[i + 8u] = static_cast<_Float16>(v[j] - static_cast<float>(hi));  // column 2 s + 1
   }
   if (threadIdx.x == 0u) tail.e[s * (cols / 256u) + b] = e;
+  tl_stamp(kTlCombineB, tl_slot + 1u);
 }
 
 // One workgroup of 256 per sequence (blockIdx.x, keys key_stride apart): the
@@ -853,16 +857,19 @@ hipError_t launch_synth_q4k_native(std::uint64_t seed, std::size_t n_blocks, flo
 #include "rtxllm/timeline.h"
 
 extern "C" hipError_t rtxllm_timeline_read(unsigned long long* host, size_t count) {
-  if (host == nullptr || count > static_cast<size_t>(rtxllm::kTlRegions) * rtxllm::kTlRegion)
-    return hipErrorInvalidValue;
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(rtxllm::g_timeline), count * sizeof(unsigned long long), 0,
-                             hipMemcpyDeviceToHost);
+  constexpr size_t kPerUnit = static_cast<size_t>(rtxllm::kTlRegions) * rtxllm::kTlRegion;
+  if (host == nullptr || count != 2u * kPerUnit) return hipErrorInvalidValue;
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(rtxllm::g_timeline), sizeof(rtxllm::g_timeline), 0,
+                                           hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  return rtxllm::timeline_read_batch(host + kPerUnit);
 }
 
 extern "C" hipError_t rtxllm_timeline_clear(void) {
   void* p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(rtxllm::g_timeline));
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(rtxllm::g_timeline));
+  if (e == hipSuccess) e = hipMemset(p, 0, sizeof(rtxllm::g_timeline));
   if (e != hipSuccess) return e;
-  return hipMemset(p, 0, sizeof(rtxllm::g_timeline));
+  return rtxllm::timeline_clear_batch();
 }
 #endif

@@ -291,6 +291,7 @@ constexpr int mm_ring() {
 // Plain output: out[pg][s][row] (pg = panel group = blockIdx.y, row stride
 // `stride`): y itself with one panel group, else the groups' partial sums.
 struct MmStore {
+  static constexpr int tl_region(int fmt) { return fmt_is_iq(fmt) ? kTlMmO : kTlMmDown; }
   float* out;
   std::uint32_t stride, batch;
   __device__ __forceinline__ void init(std::uint32_t) {}
@@ -316,6 +317,9 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   __shared__ float red[2][kMaxPanels][256];
   const std::uint32_t lane = threadIdx.x & 63u;
   const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int kTlR = TlRegionOf<Epi>::value(FMT);
+  const std::uint32_t tl_slot = ((blockIdx.y * gridDim.x + blockIdx.x) * kMaxPanels + wave) * 16u;
+  tl_stamp(kTlR, tl_slot);
   // read once, in an SGPR: a later read of the workgroup size is a vector load,
   // and its wait would also wait for the ring's loads in flight
   const std::uint32_t nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
@@ -324,6 +328,16 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t q = lane >> 4, r16 = lane & 15u;
   const std::uint32_t tiles = (rows + 15u) >> 4;
   const std::uint32_t nb = cols >> 8;  // 256-value blocks per row
+
+  // The codebook image is the first load of the wave: the barrier after its
+  // LDS fill then waits for it alone (the wait counters complete in issue
+  // order), not for the B operands and weights behind it.
+  const MmLds<FMT>* tables = nullptr;
+  MmGridStage<FMT> grid_stage;
+  if constexpr (fmt_is_iq(FMT)) {
+    tables = &mm_lds<FMT>();
+    lds_grid_issue(grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
+  }
 
   // Tile epilogue: thread t takes C elements t, t + blockDim.x, ... < 256;
   // element (lane l = e / 4, i = e % 4) is row 4 (l / 16) + i, column
@@ -394,11 +408,12 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       }
     }
   } else {
+    // block 0's operands here; the later blocks' go out after the ring's
+    // first weight loads, so the first unit waits for block 0 and its weights
+    // only
     const uint4* xb = reinterpret_cast<const uint4*>(x16) + PB * panel * 8u * 64u + lane;
 #pragma unroll
-    for (int b = 0; b < PB; ++b)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
+    for (int j = 0; j < 8; ++j) B[0][j] = xb[j * 64u];
     const X16Tail tail = x16_tail(x16, cols);
 #pragma unroll
     for (int b = 0; b < PB; ++b) fb[b] = ldexpf(1.0f, tail.e[((lane & 15u) >> 1) * nb + PB * panel + b]);
@@ -409,13 +424,6 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   const std::uint32_t prow = bpr * FmtBytes<FMT>::payload, mrow = bpr * FmtBytes<FMT>::meta;
   const Rsrc rsp = make_rsrc(w.payload, rows * prow);
   const Rsrc rsm = make_rsrc(FmtBytes<FMT>::meta > 0u ? w.meta : w.payload, rows * mrow);
-
-  const MmLds<FMT>* tables = nullptr;
-  MmGridStage<FMT> grid_stage;
-  if constexpr (fmt_is_iq(FMT)) {
-    tables = &mm_lds<FMT>();
-    lds_grid_issue(grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
-  }
 
   // (tile, block) units of this wave in order: unit u -> tile blockIdx.x +
   // (u / PB) * gridDim.x, block PB panel + u % PB. Loads past the workgroup's
@@ -433,14 +441,25 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
   };
   if (units == 0u) {  // whole workgroup: no barrier is left waiting
     epi.finish(wave, lane, nw);
+    tl_stamp(kTlR, tl_slot + 15u);
     return;
   }
   constexpr int NB = mm_ring<FMT>();
   MmRaw ring[NB];
 #pragma unroll
   for (int j = 0; j < NB - 1; ++j) load_unit(static_cast<std::uint32_t>(j), ring[j]);
+  if constexpr (!SELF) {
+    __builtin_amdgcn_sched_barrier(0);  // the ring's loads ahead of the later blocks' operands
+    const uint4* xb = reinterpret_cast<const uint4*>(x16) + PB * panel * 8u * 64u + lane;
+#pragma unroll
+    for (int b = 1; b < PB; ++b)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) B[b][j] = xb[(8u * b + j) * 64u];
+    __builtin_amdgcn_sched_barrier(0);
+  }
   if constexpr (fmt_is_iq(FMT))
     lds_grid_commit(mm_lds<FMT>(), grid_stage, mm_image<FMT>(), threadIdx.x, blockDim.x);
+  tl_stamp(kTlR, tl_slot + 1u);
   float t_post = 1.0f;
   if constexpr (!SELF) {
     if (t_eps >= 0.0f) {
@@ -453,6 +472,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
     }
   }
 
+  tl_stamp(kTlR, tl_slot + 2u);
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto finish_unit = [&](std::uint32_t u, const MmRaw& raw) {
     const int b = static_cast<int>(u % PB);
@@ -494,6 +514,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
       const std::uint32_t row = (blockIdx.x + round * gridDim.x) * 16u + 4u * (e >> 6) + (e & 3u);
       if (t_store && row < rows) epi(row, t_s, y, partner);
     }
+    tl_stamp(kTlR, tl_slot + 3u + (round < 11u ? round : 11u));
   };
 
   // unit u sits in ring slot u % NB; PERIOD units bring both the slot and the
@@ -515,6 +536,7 @@ __global__ __launch_bounds__(64 * kMaxPanels) void mm_kernel(QTensor w, const vo
     if (u0 + decltype(jc)::value < units) step(u0 + decltype(jc)::value, jc);
   });
   epi.finish(wave, lane, nw);
+  tl_stamp(kTlR, tl_slot + 15u);
 }
 
 // y[s][r] = sum over panel groups of partial[pg][s][r].
