@@ -342,6 +342,10 @@ STAGE_KERNELS = {  # decode stage -> substring of its kernel's name
     "qkv": "EpiQkv", "attention": "attn_partial_kernel", "o": "mv_kernel<10, 1, 4, false, rtxllm::(anonymous "
     "namespace)::EpiResidual", "gate_up": "EpiGateUp", "down": "mv_kernel<4, 1, 4, true", "lm_head": "EpiLogits",
 }
+BATCH8_STAGE_KERNELS = {  # batch-8 decode stage -> substring of its matrix-core kernel's name
+    "qkv": "mm_kernel<7, rtxllm::(anonymous namespace)::MmQkv", "o": "mm_kernel<7, rtxllm::MmStore",
+    "gate_up": "MmGateUp", "down": "mm_kernel<4, rtxllm::MmStore, true", "lm_head": "MmLogits",
+}
 
 
 def traffic_probe(torch) -> None:
@@ -686,43 +690,48 @@ STAGE_BYTES = {"qkv": 10854400, "attention": 16672768, "o": 7241728, "gate_up": 
 
 def counter_summary(pmc_dirs) -> str:
     """Per decode-stage kernel, the mean per dispatch of every SQ counter found
-    in the given --pmc runs of --traffic-probe, and derived figures:
-    instructions per wave; per 64 weight units (one unit per lane: a wave's
-    pass over 64 units), which is the cost per pass of the batch-1 matvecs;
-    wait / VALU-active shares of wave cycles; LDS bank conflicts per LDS-active
-    cycle. The VALU floor is the time the SIMDs need to issue the launch's
-    VALU instructions (4 cycles each on 1024 SIMDs at 2.4 GHz); the budget is
-    the time of the launch's algorithmic bytes at 70 % of 8 TB/s."""
+    in the given --pmc runs of --traffic-probe (batch-1 stages) or --mfma-probe
+    (also the batch-8 matrix-core stages, rows "<stage>_b8"), and derived
+    figures: instructions per wave; per 64 weight units (one unit per lane: a
+    wave's pass over 64 units), which is the cost per pass of the batch-1
+    matvecs; wait / VALU-active shares of wave cycles; LDS bank conflicts per
+    LDS-active cycle. The VALU floor is the time the SIMDs need to issue the
+    launch's VALU instructions (4 cycles each on 1024 SIMDs at 2.4 GHz; the
+    count includes the MFMA instructions, which occupy their pipe longer); the
+    budget is the time of the launch's algorithmic bytes at 70 % of 8 TB/s."""
     import csv
     import glob
 
+    kernels = {**STAGE_KERNELS, **{st + "_b8": k for st, k in BATCH8_STAGE_KERNELS.items()}}
     vals: dict = {}
     for d in pmc_dirs:
         for f in glob.glob(str(Path(d) / "**" / "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
-                for st, key in STAGE_KERNELS.items():
+                for st, key in kernels.items():
                     if key in r["Kernel_Name"]:
                         vals.setdefault(st, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     if not vals:
         raise SystemExit("no decode stage kernel in the counter runs")
     lines = []
-    for st in STAGE_KERNELS:
+    for st in kernels:
         if st not in vals:
             continue
         c = {k: sum(v) / len(v) for k, v in vals[st].items()}
+        base = st[:-3] if st.endswith("_b8") else st
         parts = [st] + [f"{k} {c[k]:.0f}" for k in sorted(c)]
         waves = c.get("SQ_WAVES")
         if waves:
             for k in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD", "SQ_INSTS_SMEM"):
                 if k in c:
                     parts.append(f"{k.replace('SQ_INSTS_', '').lower()}_per_wave {c[k] / waves:.1f}")
-        if st in STAGE_UNITS:
+        if st in STAGE_UNITS:  # batch 1 only
             passes = STAGE_UNITS[st] / 64.0
             for k in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD"):
                 if k in c:
                     parts.append(f"{k.replace('SQ_INSTS_', '').lower()}_per_64_units {c[k] / passes:.1f}")
         if "SQ_WAVE_CYCLES" in c and c["SQ_WAVE_CYCLES"] > 0:
-            for k in ("SQ_WAIT_ANY", "SQ_ACTIVE_INST_VALU", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS"):
+            for k in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU",
+                      "SQ_ACTIVE_INST_VMEM", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS"):
                 if k in c:
                     parts.append(f"{k.replace('SQ_', '').lower()}_share {c[k] / c['SQ_WAVE_CYCLES']:.3f}")
         if c.get("SQ_ACTIVE_INST_LDS"):
@@ -730,7 +739,7 @@ def counter_summary(pmc_dirs) -> str:
                 parts.append(f"lds_conflict_per_active {c['SQ_LDS_BANK_CONFLICT'] / c['SQ_ACTIVE_INST_LDS']:.3f}")
         if "SQ_INSTS_VALU" in c:
             floor = c["SQ_INSTS_VALU"] * VALU_CYCLES_PER_OP / (ENGINE_CLOCK_GHZ * 1e3 * SIMDS)
-            budget = STAGE_BYTES[st] / (0.7 * HBM_PEAK_GBS * 1e3)
+            budget = STAGE_BYTES[base] / (0.7 * HBM_PEAK_GBS * 1e3)
             parts.append(f"valu_floor_us {floor:.2f} budget_us_at_70pct {budget:.2f}")
         lines.append(" ".join(parts))
     return "\n".join(lines) + "\n"
