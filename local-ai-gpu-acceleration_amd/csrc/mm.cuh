@@ -170,15 +170,14 @@ __device__ __forceinline__ void mm_load(Rsrc rp, Rsrc rm, std::uint32_t vp, std:
 __device__ __forceinline__ half8 as_half8(const uint4& u) { return __builtin_bit_cast(half8, u); }
 __device__ __forceinline__ uint4 as_uint4(const half8& h) { return __builtin_bit_cast(uint4, h); }
 
-// Two fp16 integers from two 5-bit fields already placed in the low bits of
-// each 16-bit half: (1024 + v) has the bit pattern 0x6400 | v, and
-// (1024 + v) * m - 1024 m = v m, rounded once (exact: v m < 2048).
-__device__ __forceinline__ std::uint32_t small_pair_times(std::uint32_t fields, _Float16 m) {
+// Two fp16 values fma(v, f, -1024 f) of two fp16 halves v = 1024 + c: c f in
+// one rounding.
+__device__ __forceinline__ std::uint32_t code_pair_times(std::uint32_t halves, _Float16 f) {
   typedef _Float16 half2 __attribute__((ext_vector_type(2)));
-  const half2 v = __builtin_bit_cast(half2, fields | 0x64006400u);
-  const half2 mm = {m, m};
-  const half2 c = {static_cast<_Float16>(-1024.0f) * m, static_cast<_Float16>(-1024.0f) * m};
-  return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_fma(v, mm, c));
+  const half2 v = __builtin_bit_cast(half2, halves);
+  const half2 ff = {f, f};
+  const half2 c = {static_cast<_Float16>(-1024.0f) * f, static_cast<_Float16>(-1024.0f) * f};
+  return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_fma(v, ff, c));
 }
 
 // Two fp16 products w m from bytes b0, b1 of `biased` (selector 0x04010400) or
@@ -238,19 +237,29 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
     const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
     const _Float16 mf = static_cast<_Float16>(static_cast<float>(mn));
     amin = half8{mf, mf, mf, mf, mf, mf, mf, mf};
+    // Each code byte stays in place, masked to its nibble: the low nibble n
+    // (j < 4), or the high one as 16 n (j >= 4). v_perm pairs two such bytes
+    // with a high byte 0x64 into fp16 halves 1024 + n (+ 16 h for Q5_K: the
+    // qh bit at bit 4), or 1024 + 16 n (+ 256 h: the qh bit at bit 0 of the
+    // high byte). fma(half, f, -1024 f) with f = sc, or sc / 16 for the
+    // high nibbles, is then (n + 16 h) sc in one rounding (exact: < 2048, and
+    // sc / 16 and 1024 f are fp16-exact for sc < 64).
+    const _Float16 f = hi ? scf * static_cast<_Float16>(0.0625f) : scf;
     std::uint32_t out[4];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const std::uint32_t word = r.a[w + k] >> (4 * hi);  // 4 codes in the low nibble of each byte
-      std::uint32_t lo2 = __builtin_amdgcn_perm(0u, word, 0x0C010C00u) & 0x000F000Fu;  // bytes 0, 1
-      std::uint32_t hi2 = __builtin_amdgcn_perm(0u, word, 0x0C030C02u) & 0x000F000Fu;  // bytes 2, 3
+      std::uint32_t codes = r.a[w + k] & (hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+      std::uint32_t top = 0x64646464u;
       if constexpr (FMT == RTXLLM_FMT_Q5K) {
-        const std::uint32_t qb = (r.b[w + k] >> pair) & 0x01010101u;  // bit `pair` of each qh byte
-        lo2 |= (__builtin_amdgcn_perm(0u, qb, 0x0C010C00u) << 4);
-        hi2 |= (__builtin_amdgcn_perm(0u, qb, 0x0C030C02u) << 4);
+        // bit `pair` of each qh byte, rotated to bit 4 (low nibbles) or bit 0
+        // (high nibbles, into the 0x64 byte) of the same byte
+        if (hi)
+          top |= __builtin_rotateright32(r.b[w + k], pair) & 0x01010101u;
+        else
+          codes |= __builtin_rotateright32(r.b[w + k], (pair + 28u) & 31u) & 0x10101010u;
       }
-      out[2 * k] = small_pair_times(lo2, scf);
-      out[2 * k + 1] = small_pair_times(hi2, scf);
+      out[2 * k] = code_pair_times(__builtin_amdgcn_perm(top, codes, 0x05010400u), f);      // bytes 0, 1
+      out[2 * k + 1] = code_pair_times(__builtin_amdgcn_perm(top, codes, 0x07030602u), f);  // bytes 2, 3
     }
     return as_half8(make_uint4(out[0], out[1], out[2], out[3]));
   }
