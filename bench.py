@@ -1006,7 +1006,7 @@ def cpu_baseline() -> dict:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 (multi-GPU is design-only)"}))
+        print(json.dumps({"error": "bench.py measures one GPU only; run with --gpus 1 (multi-GPU is design-only)"}))
         return 2
     if args.traffic_summary:
         sys.stdout.write(traffic_summary(*args.traffic_summary))

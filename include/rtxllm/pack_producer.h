@@ -20,7 +20,7 @@
  * named <label>.q4k_payload.bin, <label>.q4k_meta.<metadata_format>.bin,
  * <label>.q4k_blocks.bin and <label>.<type>_raw_blocks.bin with label =
  * sanitize_label(tensor name) (tools/bench/native_harness.py:126-128), byte-sum
- * checksums. The "auto" Q4_K policy is this build's MI355X choice
+ * checksums. The "auto" Q4_K policy is the MI355X choice made here
  * (split-native; "auto-lossy": split-half above 65536 blocks), not the
  * reference's RTX 3060 rule (q4k_resident_pack.py:75-79); the named policies
  * are the reference's. The loaders in rtxllm/pack_manifest.h and

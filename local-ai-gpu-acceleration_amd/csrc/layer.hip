@@ -3,7 +3,7 @@
 // next-norm staging into the producing matvec, plus the Q5_K embedding gather,
 // split-context GQA attention and the greedy-token finalisation.
 //
-// The reference runtime has no Llama layer (SURVEY: its feedback kernels are
+// The reference runtime has no Llama layer (its feedback kernels are
 // unweighted RMSNorm / SiLU stand-ins, decode_kernels.cu:122-289, and its
 // attention kernels are synthetic windows); the formulas here are the
 // textbook Llama ones, restated on the CPU in oracle/rtxllm_oracle.c, with the

@@ -1,7 +1,7 @@
 // GGUF -> resident packs (host code, C++17, no GPU work). The reading of the
 // container, the tensor plan, the per-producer records and the manifests
 // follow the reference's Python producers (see include/rtxllm/pack_producer.h
-// for the file:line of each); the code is this build's own.
+// for the file:line of each); the code is written for this library.
 #include "rtxllm/pack_producer.h"
 
 #include <algorithm>

@@ -11,7 +11,7 @@ LM head), against the oracle, stage by stage:
 Why per layer: with random-init weights the 32-layer network is chaotic. A
 1e-6 relative perturbation of the oracle's own input grows to ~6e-3 after four
 layers, so no implementation that is not bit-identical to the oracle can match
-its 32-layer logits to 1e-3; the per-stage comparison bounds this build's own
+its 32-layer logits to 1e-3; the per-stage comparison bounds the GPU step's own
 error per layer instead (worst layer 2.99e-4 with the seeds below). All calls go
 through the C-ABI."""
 
