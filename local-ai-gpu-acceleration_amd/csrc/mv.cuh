@@ -548,8 +548,10 @@ __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u
       lo[i] = r.a[i] & 0x0F0F0F0Fu;
       hi[i] = (r.a[i] >> 4) & 0x0F0F0F0Fu;
       if constexpr (FMT == RTXLLM_FMT_Q5K) {
-        lo[i] |= ((r.c[i] >> (2u * g)) & 0x01010101u) << 4;
-        hi[i] |= ((r.c[i] >> (2u * g + 1u)) & 0x01010101u) << 4;
+        // bit 2 g (low nibbles) / 2 g + 1 (high nibbles) of each qh byte,
+        // rotated to bit 4 of the same byte: one funnel shift and one and-or
+        lo[i] |= __builtin_rotateright32(r.c[i], (2u * g + 28u) & 31u) & 0x10101010u;
+        hi[i] |= __builtin_rotateright32(r.c[i], (2u * g + 29u) & 31u) & 0x10101010u;
       }
     }
     float s0, m0, s1, m1;
