@@ -197,14 +197,19 @@ template <int FMT>
 __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, int j, std::uint32_t q,
                                            half8& amin) {
   if constexpr (FMT == RTXLLM_FMT_IQ2S) {
-    const std::uint32_t qsb = (r.a[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    // grid index qs[j] | (qh >> 2 (j & 3) & 3) << 8: the qh byte's four 2-bit
+    // fields spread one per byte, and one v_perm lays the index pair (j, j ^ 1)
+    // into the two 16-bit halves (both computed once per word / pair)
     const std::uint32_t qh = (std::uint32_t{r.s[1]} >> (8 * (j >> 2))) & 0xFFu;  // qh of sub-block 2 q + j / 4
-    const std::uint32_t idx = qsb | (((qh >> (2 * (j & 3))) & 3u) << 8);
+    const std::uint32_t s6 = (qh << 6) | qh;
+    const std::uint32_t hb = ((s6 << 12) | s6) & 0x03030303u;
+    const std::uint32_t ip = __builtin_amdgcn_perm(hb, r.a[j >> 2], (j & 2) ? 0x07030602u : 0x05010400u);
+    const std::uint32_t idx = (j & 1) ? ip >> 16 : ip & 0xFFFFu;
     const std::uint32_t sgb = (r.a[2 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
     const uint2 g = t->grid2b[idx];
     const uint2 sm = t->sign[sgb];
     const std::uint32_t nib = ((std::uint32_t{r.s[2]} >> (8 * (j >> 2))) >> (4 * ((j & 3) >> 1))) & 15u;
-    const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
+    const _Float16 m = static_cast<_Float16>(static_cast<std::uint16_t>(2u * nib + 1u));  // one v_cvt_f16_u16
     const std::uint32_t b0 = (g.x ^ sm.x) | 0x01010101u, b1 = (g.y ^ sm.y) | 0x01010101u;
     return as_half8(make_uint4(mm_biased_pair(b0, 0x04010400u, m), mm_biased_pair(b0, 0x04030402u, m),
                                mm_biased_pair(b1, 0x04010400u, m), mm_biased_pair(b1, 0x04030402u, m)));
@@ -219,7 +224,7 @@ __device__ __forceinline__ half8 mm_decode(const MmRaw& r, const MmLds<FMT>* t, 
     const std::uint32_t g0 = t->grid3b[i0], g1 = t->grid3b[i1];
     const uint2 sm = t->sign[sgb];
     const std::uint32_t nib = (std::uint32_t{r.s8} >> (4u * sub)) & 15u;
-    const _Float16 m = static_cast<_Float16>(static_cast<float>(2u * nib + 1u));
+    const _Float16 m = static_cast<_Float16>(static_cast<std::uint16_t>(2u * nib + 1u));  // one v_cvt_f16_u16
     const std::uint32_t b0 = (g0 ^ sm.x) | 0x01010101u, b1 = (g1 ^ sm.y) | 0x01010101u;
     return as_half8(make_uint4(mm_biased_pair(b0, 0x04010400u, m), mm_biased_pair(b0, 0x04030402u, m),
                                mm_biased_pair(b1, 0x04010400u, m), mm_biased_pair(b1, 0x04030402u, m)));
