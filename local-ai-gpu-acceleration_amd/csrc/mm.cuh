@@ -168,7 +168,6 @@ __device__ __forceinline__ void mm_load(Rsrc rp, Rsrc rm, std::uint32_t vp, std:
 }
 
 __device__ __forceinline__ half8 as_half8(const uint4& u) { return __builtin_bit_cast(half8, u); }
-__device__ __forceinline__ uint4 as_uint4(const half8& h) { return __builtin_bit_cast(uint4, h); }
 
 // Two fp16 values fma(v, f, -1024 f) of two fp16 halves v = 1024 + c: c f in
 // one rounding.
