@@ -1,5 +1,5 @@
 """GPU parity of the batch decode step (8 sequences through the same weights
-on the matrix cores) against the oracle at a small Llama shape: every
+on the matrix cores; 2, 3, 5 and 7 as well) against the oracle at a small Llama shape: every
 sequence, with its own token, position and KV pages (one permutation of all
 the batch's pages, so sequences interleave in the cache), matches the
 oracle's batch-1 step for that sequence within 1e-3 normwise on logits and
@@ -69,6 +69,19 @@ def test_batch_step_matches_oracle_per_sequence(orc, model):
     check_step(orc, model, SMALL_B)
 
 
+@pytest.mark.parametrize("batch", [2, 3, 5, 7])
+def test_batch_step_matches_oracle_at_smaller_batches(orc, batch):
+    """2-7 sequences: the matrix-core operands' unused columns (sequences past
+    the batch) stay zero, the attention grid, the staging and the argmax keys
+    follow the batch, and every sequence still matches the oracle."""
+    s = Shape(**{**SMALL_B.__dict__, "batch": batch})
+    m = build(s, SEED + batch)
+    try:
+        check_step(orc, m, s)
+    finally:
+        m.close()
+
+
 def test_batch_step_wide_ffn_panel_groups(orc):
     """ffn 4608 > 4096 columns: the down projection splits into two panel
     groups, whose partial sums the residual staging adds per sequence."""
@@ -82,18 +95,20 @@ def test_batch_step_wide_ffn_panel_groups(orc):
 
 
 def check_step(orc, m, s):
-    m.set_token_pos(TOKENS, POSITIONS)
+    b = s.batch
+    tok, pos = TOKENS[:b], POSITIONS[:b]
+    m.set_token_pos(tok, pos)
     ref = HostModel(m, range(s.n_layers))
     k_before = {l: ref.L[l]["k_cache"].copy() for l in range(s.n_layers)}
     v_before = {l: ref.L[l]["v_cache"].copy() for l in range(s.n_layers)}
     m.step()
     torch.cuda.synchronize()
-    h = m.download("h", np.float32).reshape(B, s.hidden)
-    logits = m.download("logits", np.float32).reshape(B, s.vocab)
+    h = m.download("h", np.float32).reshape(b, s.hidden)
+    logits = m.download("logits", np.float32).reshape(b, s.vocab)
     tokens = m.download("token", np.uint32)
-    assert list(m.download("pos", np.uint32)) == [p + 1 for p in POSITIONS]
-    for q in range(B):
-        h_ref, logits_ref = ref.run(orc, ref.embed_row(orc, TOKENS[q]), POSITIONS[q], seq=q)
+    assert list(m.download("pos", np.uint32)) == [p + 1 for p in pos]
+    for q in range(b):
+        h_ref, logits_ref = ref.run(orc, ref.embed_row(orc, tok[q]), pos[q], seq=q)
         assert rel(h[q], h_ref) <= TOL, (q, rel(h[q], h_ref))
         assert rel(logits[q], logits_ref) <= TOL, (q, rel(logits[q], logits_ref))
         assert int(tokens[q]) == int(np.argmax(logits[q]))  # the GPU's argmax of its own logits
@@ -109,10 +124,10 @@ def check_step(orc, m, s):
         rk = ref.L[l]["k_cache"].view(np.float16).astype(np.float32)
         rv = ref.L[l]["v_cache"].view(np.float16).astype(np.float32)
         mask = np.ones(kc.size, bool)
-        for q in range(B):
+        for q in range(b):
             row = table[q * pps:(q + 1) * pps]
             for g in range(s.n_kv_heads):
-                o = kv_slot(m, POSITIONS[q], g, row)
+                o = kv_slot(m, pos[q], g, row)
                 assert rel(kf[o:o + HEAD_DIM], rk[o:o + HEAD_DIM]) <= 4e-3, (l, q, g)
                 assert rel(vf[o:o + HEAD_DIM], rv[o:o + HEAD_DIM]) <= 4e-3, (l, q, g)
                 mask[o:o + HEAD_DIM] = False
