@@ -52,6 +52,15 @@ def references(orc, pack, x):
     return y32, y64
 
 
+def references_staged(orc, pack, x):
+    """(fp32 sequential, float64, float64 on the staged x) products of the pack
+    with x: the last multiplies the batch-1 kernels' 22-bit staged activation
+    (xq.h: one power-of-two scale per 16-value group) exactly."""
+    y32, y64 = references(orc, pack, x)
+    of, pl, mt = oracle_args(pack)
+    return y32, y64, orc.matvec_staged_f64(of, pl, mt, x, pack.rows, pack.cols, THREADS)
+
+
 def activation(kind: str, cols: int, seed: int) -> np.ndarray:
     x = packs.normal_f32(seed, cols)
     if kind == "outlier":
@@ -98,10 +107,13 @@ def batch_staged(x: np.ndarray) -> np.ndarray:
 
 
 def gate_staged(label: str, y: np.ndarray, y32: np.ndarray, y64: np.ndarray, yst64: np.ndarray) -> tuple[float, float]:
-    """Gate of a kernel that rounds its activation once on input (the batched
-    matrix-core matvec keeps ~22 bits per 256-value block, so a block whose
-    values span many decades loses the small ones' low bits; fp32 keeps 24
-    bits per value). yst64 is the float64 product with the rounded activation.
+    """Gate of a kernel that rounds its activation once on input (the batch-1
+    kernels keep 22 bits per 16-value group, the batched matrix-core matvec
+    ~22 bits per 256-value block, so a group whose values span many decades
+    loses the small ones' low bits; fp32 keeps 24 bits per value). On
+    heavy-tailed activations that rounding alone can exceed twice the fp32
+    path's per-element error. yst64 is the float64 product with the rounded
+    activation.
       * the kernel's arithmetic on its rounded input: both measures of y
         against yst64 at most GATE times the fp32-sequential path's against y64;
       * normwise against y64 at most GATE times the fp32-sequential path's;

@@ -8,10 +8,12 @@ picks the one the runner picks):
     handing column-split partials over through bounded LDS waits (K-quant or
     GGUF IQ gate/up at hidden <= 4096);
   * mv_kernel with per-wave inputs (hidden > 4096).
-Each is held to the float64 gate of tests/precision_ref.py (normwise and per
-element, at most 2x the reference's own fp32 sequential path,
-main.cpp:1261-1309) at the 8B FFN shapes, for N(0,1), outlier and
-heavy-tailed activations: the plain matvec on the matrix cores
+Each is held to the staged float64 gate of tests/precision_ref.py
+(gate_staged: the kernel's arithmetic against the float64 product of its
+22-bit staged activation, and the result against the float64 product of x,
+at most 2x the reference's own fp32 sequential path, main.cpp:1261-1309, or
+2x the staging's own error where that is larger) at the 8B FFN shapes, for
+N(0,1), outlier and heavy-tailed activations: the plain matvec on the matrix cores
 (rtxllm_matvec_xq_mfma) on y = W x, and the fused stage on act = silu(g) u
 with g, u from the float64 and fp32-sequential products. The bounded waits'
 status bit is checked in both directions: 0 after every normal launch, and
@@ -29,7 +31,7 @@ from rtxllm_amd import formats as F  # noqa: E402
 from rtxllm_amd import ops, packs  # noqa: E402
 from rtxllm_amd._lib import lib  # noqa: E402
 
-from precision_ref import KINDS, activation, gate, references  # noqa: E402
+from precision_ref import KINDS, activation, gate_staged, references_staged  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -96,10 +98,10 @@ def test_mfma_matvec_f64_gate(orc, case):
     dev = ops.DevicePack(pack)
     for kind in KINDS:
         x = activation(kind, cols, 0x5EED0B10 + cols + fmt)
-        y32, y64 = references(orc, pack, x)
+        y32, y64, yst64 = references_staged(orc, pack, x)
         xq = ops.stage(ops.to_dev(x))
         y = mfma_matvec(dev, xq)
-        gate(f"mfma {cid(case)} {kind}", y, y32, y64)
+        gate_staged(f"mfma {cid(case)} {kind}", y, y32, y64, yst64)
         y_dot = ops.matvec_xq(dev, xq).cpu().numpy()
         d = float(np.max(np.abs(y.astype(np.float64) - y_dot)) / np.max(np.abs(y64)))
         print(f"  mfma vs v_dot4 kernel: {d:.3e}")
@@ -131,13 +133,14 @@ def test_gate_up_silu_f64_gate(orc, case):
     dev = ops.DevicePack(pack)
     for kind in KINDS:
         x = activation(kind, cols, 0x5EED0C10 + cols + fmt)
-        y32, y64 = references(orc, pack, x)
+        y32, y64, yst64 = references_staged(orc, pack, x)
         act32 = silu32(y32[0::2]) * y32[1::2]
         act64 = silu64(y64[0::2]) * y64[1::2]
+        actst64 = silu64(yst64[0::2]) * yst64[1::2]
         act, status = gate_up(dev, ops.stage(ops.to_dev(x)))
         assert status == 0
         assert np.all(np.isfinite(act))
-        gate(f"gate_up {cid(case)} {kind}", act, act32, act64)
+        gate_staged(f"gate_up {cid(case)} {kind}", act, act32, act64, actst64)
 
 
 def test_gate_up_wait_timeout_sets_status(orc):

@@ -9,7 +9,12 @@ oracle's fp32 sequential accumulation (main.cpp:1261-1309). The bar is
 
 and the same for the per-element relative error with a floor of 1e-3 of
 max|y64| (tests/precision_ref.py), at the config shapes for every format, with N(0,1), outlier (one 1e3 value per
-16-value group) and heavy-tailed activations. Also: a NaN activation poisons
+16-value group) and heavy-tailed activations. Every kernel rounds its activation
+once on input (22 bits per 16-value group at batch 1, per 256-value block in the
+batched matvec), so each is gated as gate_staged states: its arithmetic against
+the float64 product of the rounded activation within the bar, and per element
+against y64 within 2x the larger of the fp32 path's and the rounding's own
+error (on heavy-tailed activations the rounding alone can exceed the bar). Also: a NaN activation poisons
 the outputs as in fp32, and the device fp16 decode of d / dmin follows the
 reference's rule (main.cpp:1086-1098) for subnormal, signed-zero, infinite and
 NaN codes, bit for bit against the oracle's dequant."""
@@ -27,7 +32,8 @@ from rtxllm_amd._lib import lib  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-from precision_ref import GATE, activation, batch_staged, elem64, err64, gate, gate_staged, oracle_args, references  # noqa: E402,F401
+from precision_ref import (GATE, activation, batch_staged, elem64, err64, gate, gate_staged, oracle_args,  # noqa: E402,F401
+                           references, references_staged)
 
 
 CONFIG_CASES = (
@@ -50,12 +56,12 @@ def test_matvec_f64_gate_config_shapes(orc, case):
     dev = ops.DevicePack(pack)
     for kind in ("normal", "outlier", "heavy"):
         x = activation(kind, cols, 0x5EED0100 + cols + fmt)
-        y32, y64 = references(orc, pack, x)
+        y32, y64, yst64 = references_staged(orc, pack, x)
         xd = ops.to_dev(x)
         y = ops.matvec(dev, xd).cpu().numpy()
         y_xq = ops.matvec_xq(dev, ops.stage(xd)).cpu().numpy()
         assert np.array_equal(y.view(np.uint32), y_xq.view(np.uint32))
-        gate(f"{case_id(case)} {kind}", y, y32, y64)
+        gate_staged(f"{case_id(case)} {kind}", y, y32, y64, yst64)
 
 
 DECODE_NAMES = {
@@ -100,9 +106,9 @@ def test_reference_named_launchers_f64_gate(orc, fmt):
     dev = ops.DevicePack(pack)
     for kind in ("normal", "outlier"):
         x = activation(kind, cols, 0x5EED0300 + fmt)
-        y32, y64 = references(orc, pack, x)
+        y32, y64, yst64 = references_staged(orc, pack, x)
         logits, _, _ = run_decode_launcher(fmt, dev, x, rows, cols)
-        gate(f"{F.NAMES[fmt]} {kind}", logits, y32, y64)
+        gate_staged(f"{F.NAMES[fmt]} {kind}", logits, y32, y64, yst64)
 
 
 @pytest.mark.parametrize("fmt", [F.Q4K_SPLIT_NATIVE, F.Q5K, F.IQ2S, F.IQ3S, F.IQ3S_UNITS],
