@@ -263,9 +263,17 @@ __device__ __forceinline__ float h2f(std::uint32_t bits) {
 // Byte offsets, relative to the start of a row, of the fields lane's unit
 // (block b, unit k) reads; fixed for the whole launch. Rows are addressed by a
 // wave-uniform base pointer, so every load is (uniform base + lane offset).
+// The byte choice of kq_head_scales for a lane's 64-value group g (fixed for
+// the launch): a v_perm selector for head words 1-2 and one for word 3, the
+// shift and the mask of the word 1-2 bytes.
+struct KqHeadSel {
+  std::uint32_t sel12, sel3, sh, mask;
+};
+
 struct UnitOff {
   std::uint32_t o[5];
   std::uint32_t g;      // K-quants: 64-value group k >> 1
+  KqHeadSel hs;         // K-quants with the native head
 };
 
 template <int FMT>
@@ -309,6 +317,16 @@ __device__ __forceinline__ UnitOff unit_offsets(std::uint32_t b, std::uint32_t k
   UnitOff u{};
   const std::uint32_t pb = b * FmtBytes<FMT>::payload, mb = b * FmtBytes<FMT>::meta, g = k >> 1;
   u.g = g;
+  // sub-blocks 2g, 2g + 1: bytes i, i + 1 (i = 2 (g & 1)) of head words 1-3
+  const std::uint32_t i2 = 0x02020202u * (g & 1u);
+  u.hs.sel12 = 0x05040100u + i2;                         // (w1 byte i, i + 1, w2 byte i, i + 1)
+  u.hs.sel3 = g < 2u ? 0x0C0C0C0Cu : 0x01000100u + i2;  // zeros / (w3 byte i, i + 1, i, i + 1)
+  u.hs.sh = g < 2u ? 0u : 2u;
+  u.hs.mask = g < 2u ? 0x3F3F3F3Fu : 0x30303030u;
+  // opaque to the compiler: from the two constants it would learn that bits
+  // 6-7 of each scale byte are zero and turn the byte-to-float conversions
+  // (v_cvt_f32_ubyte1-3, one instruction each) into bit-field extracts first
+  asm("" : "+v"(u.hs.mask));
   if constexpr (FMT == RTXLLM_FMT_IQ2S_UNITS) {
     u.o[0] = 64u * b + 8u * k;             // qs, signs of the unit
     u.o[1] = 64u * nb + 16u * b + 2u * k;  // qh, scales of the unit
@@ -426,24 +444,20 @@ __device__ __forceinline__ void unit_load(Rsrc rp, Rsrc rm, std::uint32_t sp, st
   }
 }
 
-// (S, M) of sub-blocks 2g and 2g+1 from the native 16-byte head (d, dmin, 12
-// packed 6-bit scale/min bytes), branch-free: all eight scales and mins are
-// unpacked byte-parallel (get_scale_min_k4 for j < 4 and j >= 4), then the
-// lane's two bytes are picked by its fixed group g.
-__device__ __forceinline__ void kq_head_pairs(const std::uint32_t h[4], std::uint32_t g, float& s0, float& m0,
-                                              float& s1, float& m1) {
-  const std::uint32_t sc03 = h[1] & 0x3F3F3F3Fu;
-  const std::uint32_t m03 = h[2] & 0x3F3F3F3Fu;
-  const std::uint32_t sc47 = (h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u);
-  const std::uint32_t m47 = ((h[3] >> 4) & 0x0F0F0F0Fu) | ((h[2] >> 2) & 0x30303030u);
-  const std::uint32_t sh = 16u * (g & 1u);
-  const std::uint32_t sc = (g < 2u ? sc03 : sc47) >> sh;
-  const std::uint32_t mn = (g < 2u ? m03 : m47) >> sh;
-  const float d = h2f(h[0]), dmin = h2f(h[0] >> 16);
-  s0 = d * static_cast<float>(sc & 0xFFu);
-  s1 = d * static_cast<float>((sc >> 8) & 0xFFu);
-  m0 = dmin * static_cast<float>(mn & 0xFFu);
-  m1 = dmin * static_cast<float>((mn >> 8) & 0xFFu);
+// The 6-bit scales and mins of sub-blocks j = 2g, 2g + 1 from the native
+// 16-byte head (d, dmin, 12 packed scale/min bytes q), as get_scale_min_k4
+// unpacks them, in one word: bytes (sc_2g, sc_2g+1, m_2g, m_2g+1). With i = 2
+// (g & 1) and head words w1 = q[0..3], w2 = q[4..7], w3 = q[8..11]:
+//  * g < 2: sc_j = q[j] & 63, m_j = q[j + 4] & 63 (bytes i, i + 1 of w1, w2);
+//  * g >= 2: sc_j = (q[j + 4] & 15) | (q[j - 4] >> 6) << 4, m_j = q[j + 4] >> 4
+//    | (q[j] >> 6) << 4: the low / high nibbles of w3 bytes i, i + 1 under the
+//    top two bits of w1 / w2 bytes i, i + 1.
+// One perm gathers the w1 / w2 bytes and one the w3 bytes (zeros for g < 2)
+// by the lane's fixed selectors, so no lane unpacks bytes it does not use.
+__device__ __forceinline__ std::uint32_t kq_head_scales(const std::uint32_t h[4], const KqHeadSel& s) {
+  const std::uint32_t w12 = (__builtin_amdgcn_perm(h[2], h[1], s.sel12) >> s.sh) & s.mask;
+  const std::uint32_t w3 = __builtin_amdgcn_perm(h[3], h[3], s.sel3);
+  return w12 | (w3 & 0x00000F0Fu) | ((w3 >> 4) & 0x0F0F0000u);
 }
 
 // The IQ scale byte: beside qh in one 16-bit field in the unit layouts, its
@@ -554,10 +568,21 @@ __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u
         hi[i] |= __builtin_rotateright32(r.c[i], (2u * g + 29u) & 31u) & 0x10101010u;
       }
     }
-    float s0, m0, s1, m1;
+    const float c0 = static_cast<float>(dot16(lo, x0));
+    const float c1 = static_cast<float>(dot16(hi, x1));
     if constexpr (FMT == RTXLLM_FMT_Q4K_RAW || FMT == RTXLLM_FMT_Q4K_SPLIT_NATIVE || FMT == RTXLLM_FMT_Q5K) {
-      kq_head_pairs(r.b, g, s0, m0, s1, m1);
-    } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
+      // d (sc0 s0 c0 + sc1 s1 c1) - dmin (m0 sum0 + m1 sum1): the group scales
+      // s are powers of two, so sc s is exact
+      const std::uint32_t sm = kq_head_scales(r.b, u.hs);
+      const float d = h2f(r.b[0]), dmin = h2f(r.b[0] >> 16);
+      const float p = __builtin_fmaf(static_cast<float>((sm >> 8) & 0xFFu) * x1.s, c1,
+                                     (static_cast<float>(sm & 0xFFu) * x0.s) * c0);
+      const float q = __builtin_fmaf(static_cast<float>(sm >> 24), x1.sum,
+                                     static_cast<float>((sm >> 16) & 0xFFu) * x0.sum);
+      return __builtin_fmaf(-dmin, q, d * p);
+    }
+    float s0, m0, s1, m1;
+    if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_PREDECODED || FMT == RTXLLM_FMT_Q4K_RAW_PREDECODED) {
       s0 = __uint_as_float(r.b[0]), m0 = __uint_as_float(r.b[1]);
       s1 = __uint_as_float(r.b[2]), m1 = __uint_as_float(r.b[3]);
     } else if constexpr (FMT == RTXLLM_FMT_Q4K_SPLIT_HALF) {
@@ -568,8 +593,6 @@ __device__ __forceinline__ float unit_compute(const UnitRaw& r, const UnitOff& u
       s0 = d * static_cast<float>(r.b[1] & 0xFFu), s1 = d * static_cast<float>(r.b[1] >> 8);
       m0 = dmin * static_cast<float>(r.b[2] & 0xFFu), m1 = dmin * static_cast<float>(r.b[2] >> 8);
     }
-    const float c0 = static_cast<float>(dot16(lo, x0));
-    const float c1 = static_cast<float>(dot16(hi, x1));
     return ((s0 * x0.s) * c0 - m0 * x0.sum) + ((s1 * x1.s) * c1 - m1 * x1.sum);
   }
 }
