@@ -580,6 +580,14 @@ def timeline(torch) -> str:
                    f"gate_up per wave: entry to codebook barrier {med(g[:, 1] - g[:, 0]):.2f}, rounds "
                    + ", ".join(f"{med(g[g[:, k + 1] > 0, k + 1] - g[g[:, k + 1] > 0, k]):.2f}" for k in range(1, 5)
                                if (g[:, k + 1] > 0).any()))
+        # down: entry / end in region 5, the self-staging point in region 9, same slot
+        d = reg(b, 5, 2)
+        st = b[9 * TL_REGION:9 * TL_REGION + d.shape[0]]
+        ok = (d[:, 0] > 0) & (st > 0)
+        if ok.any():
+            out.append(f"  down per wave: entry to activation staged {med(st[ok] - d[ok, 0]):.2f} "
+                       f"(p90 {np.percentile(st[ok] - d[ok, 0], 90) * TL_US:.2f}), staged to end "
+                       f"{med(d[ok, 1] - st[ok]):.2f}")
         lm = reg(b, 6, 2)
         slots = np.nonzero(lm[:, 0] > 0)[0]
         t0 = reg(b, 3, 2)[:, 0]

@@ -934,6 +934,7 @@ __global__ __launch_bounds__(64 * EpiWaves<Epi>::value) void mv_kernel(QTensor w
       xg_quant(xf0[i], x0[i]);
       xg_quant(xf1[i], x1[i]);
     }
+    tl_stamp(kTlR >= 0 ? kTlSelfStaged : -1, tl_slot / 2u);
   }
   if constexpr (kPair) {
     ready[wave] = 0u;

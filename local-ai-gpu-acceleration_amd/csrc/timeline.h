@@ -22,6 +22,9 @@
 //   the batch matvecs kTlMm* ((panel group * workgroups + workgroup) * 8 +
 //                   wave) * 16 + p: entry, codebook barrier passed, RMSNorm
 //                   scale ready, tiles 0 .. 11 done (p = 3 .. 14), end;
+//   kTlSelfStaged   workgroup * waves_max + wave: a self-staging matvec wave
+//                   has staged its activation groups (the kernel's own region
+//                   holds its entry and end);
 //   kTlRmsStage*    ((seq * blocks + block) * 4 + wave) * 2 + p: entry, end,
 //                   after the o projection (groups = 1) and after the down
 //                   projection or the embedding (others).
@@ -45,6 +48,7 @@ enum TlRegion : int {
   kTlLogits = 6,
   kTlAttnPartialB = 7,
   kTlCombineB = 8,
+  kTlSelfStaged = 9,
   kTlRegions = 16,  // per translation unit
   kTlMmQkv = 16,
   kTlMmO = 17,
