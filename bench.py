@@ -855,16 +855,18 @@ def units_sweep(torch) -> dict:
     return out
 
 
+READ_MODES = {0: "grid-stride x4", 1: "grid-stride x8", 2: "chunk per workgroup x4"}
 READ_SIZES = {"o": 7241728, "qkv": 10854400, "attention": 16777216, "iq2s_14336x4096": 18882560,
               "down": 33103872, "gate_up": 37748736, "lm_head": 361698304}
 
 
 def read_ceiling(torch) -> dict:
     """What a plain streaming read of the same bytes takes on this GPU
-    (rtxllm_stream_read: 16-byte nontemporal loads, four in flight per lane,
-    the best of four grid sizes), one launch per buffer over rotating buffers
-    spanning more than twice the MALL (HBM-cold), in a hipGraph like the
-    stages."""
+    (rtxllm_stream_read: 16-byte nontemporal loads; the best of three access
+    patterns, grid-stride with four or eight loads in flight per lane or one
+    contiguous chunk per workgroup, at five grid sizes), one launch per buffer
+    over rotating buffers spanning more than twice the MALL (HBM-cold), in a
+    hipGraph like the stages."""
     from rtxllm_amd._lib import check, probe_lib
 
     stream = torch.cuda.Stream()
@@ -875,17 +877,19 @@ def read_ceiling(torch) -> dict:
         bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0") for _ in range(k)]
         res = torch.empty(16384, dtype=torch.int32, device="cuda:0")
         best = None
-        for grid in (1024, 2048, 4096, 8192):
-            def run(grid=grid):
-                for b in bufs:
-                    check("rtxllm_stream_read", probe_lib().rtxllm_stream_read(b.data_ptr(), nbytes, res.data_ptr(), grid,
-                                                                          sp))
+        for mode in READ_MODES:
+            for grid in (512, 1024, 2048, 4096, 8192):
+                def run(grid=grid, mode=mode):
+                    for b in bufs:
+                        check("rtxllm_stream_read", probe_lib().rtxllm_stream_read(b.data_ptr(), nbytes, res.data_ptr(),
+                                                                              grid, mode, sp))
 
-            us = time_graph(torch, stream, run, reps=5) * 1e3 / k
-            best = (us, grid) if best is None or us < best[0] else best
-        us, grid = best
+                us = time_graph(torch, stream, run, reps=5) * 1e3 / k
+                best = (us, grid, mode) if best is None or us < best[0] else best
+        us, grid, mode = best
         out[name] = {"bytes": nbytes, "us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
-                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "workgroups": grid}
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "workgroups": grid,
+                     "pattern": READ_MODES[mode]}
         del bufs, res
         torch.cuda.empty_cache()
     return out

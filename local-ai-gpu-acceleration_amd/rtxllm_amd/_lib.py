@@ -161,7 +161,7 @@ def probe_lib() -> ctypes.CDLL:
             raise RuntimeError(f"{PROBE_LIB_PATH} is missing: build it with `make -C {PKG_ROOT}`")
         handle = ctypes.CDLL(os.fspath(PROBE_LIB_PATH))
         handle.rtxllm_stream_read.restype = c_int
-        handle.rtxllm_stream_read.argtypes = [_P, c_size_t, _P, _U, _S]
+        handle.rtxllm_stream_read.argtypes = [_P, c_size_t, _P, _U, _U, _S]
         _probe = handle
     return _probe
 
